@@ -1,0 +1,562 @@
+// cx_expert.hip — grouped fp8 block-scaled expert MLP for gfx950.
+//
+// Computes, for every (token, expert) pair of a plan,
+//   h = silu(Wg . x) * (Wu . x)          (fp32, k-block scales applied in fp32)
+//   y_pair = Wd . h                       (fp32)
+// and combines y[t] = sum_k w_k * y_pair(t,k) + y_pair(t, shared).
+// Semantics: RunFusedUpGateReferenceV2 / RunDownReferenceV2
+// (expert_node_v2/backend/expert_reference_v2.cc:11-144) and the fp32 combine
+// of combine_outputs_torch (server/moe_layer_runtime.py:148-167).
+//
+// Design (MI355X-first, not a translation of the CUDA matvecs):
+//  * The fp8 weights are streamed once per launch in their uploaded row-major
+//    layout with dwordx4 loads (each lane reads 32 contiguous bytes of one row
+//    per 128-column k-block; 16 lanes x 4 groups cover a 16x128 tile = 2 KB).
+//  * They are converted in registers to bf16 (or fp16 when the activations
+//    are fp16) by the gfx950 converter v_cvt_scalef32_pk_{bf16,f16}_fp8 —
+//    exact, e4m3 fits both — and fed to v_mfma_f32_16x16x32_{bf16,f16} with
+//    the tokens of one expert as the 16 MFMA columns.  Even at one token per
+//    expert the matrix cores do the multiply-adds, leaving the VALU only the
+//    conversion (0.5 op per weight byte) and the per-k-block scale FMA.
+//  * The 128x128 block scale is uniform over a 16-row x 128-column MFMA tile,
+//    so each k-block's 4 MFMAs accumulate into a fresh fp32 tile that is then
+//    scaled and added to the running fp32 accumulator: dequantise-then-fp32
+//    exactly, products of exact bf16/fp16 values accumulated in fp32.
+//  * h stays fp32; the down projection consumes it as a two-term bf16 split
+//    (h = hi + lo, |h - hi - lo| <= 2^-17 |h|) with two MFMAs per step.
+//  * The k order inside a k-block is permuted identically for the weight
+//    (A) and activation (B) operands, so any lane->k assignment of the MFMA
+//    is valid; loads stay contiguous.
+#include "cx_internal.h"
+
+namespace cx {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8 cvt8_bf16(uint32_t w0, uint32_t w1) {
+    const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false);
+    const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true);
+    const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
+    const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
+    return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+__device__ __forceinline__ f16x8 cvt8_f16(uint32_t w0, uint32_t w1) {
+    const f16x2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false);
+    const f16x2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true);
+    const f16x2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false);
+    const f16x2 d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true);
+    return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+template <bool F16>
+struct Mma;
+
+template <>
+struct Mma<false> {
+    typedef bf16x8 V;
+    static __device__ __forceinline__ V cvt(uint32_t a, uint32_t b) { return cvt8_bf16(a, b); }
+    static __device__ __forceinline__ V bits(u32x4 v) { return __builtin_bit_cast(V, v); }
+    static __device__ __forceinline__ f32x4 mma(V a, V b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct Mma<true> {
+    typedef f16x8 V;
+    static __device__ __forceinline__ V cvt(uint32_t a, uint32_t b) { return cvt8_f16(a, b); }
+    static __device__ __forceinline__ V bits(u32x4 v) { return __builtin_bit_cast(V, v); }
+    static __device__ __forceinline__ f32x4 mma(V a, V b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+
+// fp32 -> bf16 bits, round to nearest even (finite inputs; NaN kept quiet).
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t f16_rne(float f) {
+    const _Float16 h = static_cast<_Float16>(f);  // v_cvt_f16_f32: RNE
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h));
+}
+
+__device__ __forceinline__ uint32_t cast_out(float f, int out_dtype) {
+    return out_dtype == CX_DTYPE_FP16 ? f16_rne(f) : bf16_rne(f);
+}
+
+// Resolves the work unit of this workgroup.  Returns false if the
+// workgroup has no work (grid is sized for the worst case).
+struct Unit {
+    cx_expert_desc e;
+    int pb;  // first pair
+    int np;  // pairs in this unit
+};
+
+__device__ __forceinline__ bool resolve_unit(const ExpertLaunch& L, int unit_cap, Unit* u) {
+    const int item = blockIdx.y;
+    if (L.table != nullptr) {
+        if (item >= L.plan.hdr->n_items) return false;
+        const int slot = L.plan.item_slot[item];
+        u->pb = L.plan.item_pair_begin[item];
+        u->np = L.plan.item_pair_count[item];
+        u->e = L.table[L.plan.slot_expert[slot]];
+    } else {
+        u->pb = item * unit_cap;
+        if (u->pb >= L.n_tokens) return false;
+        u->np = min(unit_cap, L.n_tokens - u->pb);
+        u->e = L.single;
+    }
+    return u->np > 0;
+}
+
+__device__ __forceinline__ int pair_token(const ExpertLaunch& L, int p) {
+    return L.table != nullptr ? L.plan.pair_token[p] : p;
+}
+
+// ---------------------------------------------------------------------------
+// Phase A: gate/up.  Workgroup = 16 rows of gate and up of one expert, all
+// pairs of one work item (<= 16*MAXT), K split over the 4 waves; the four
+// partial tiles are summed in LDS in a fixed order.
+// grid = (inter/16, max_items), block = 256.
+template <int MAXT, bool F16>
+__global__ __launch_bounds__(256) void k_gate_up(ExpertLaunch L) {
+    typedef Mma<F16> M;
+    typedef typename M::V V;
+    Unit u;
+    if (!resolve_unit(L, kTileTok * MAXT, &u)) return;
+    const int H = u.e.hidden, I = u.e.inter;
+    const int r0 = blockIdx.x * kTileRows;
+    if (r0 >= I) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int g = lane >> 4, c = lane & 15;
+    const int nkb = H / kKB;
+    const int kb0 = (wave * nkb) / kWaves, kb1 = ((wave + 1) * nkb) / kWaves;
+
+    const size_t roff = (size_t)(r0 + c) * H + g * 32;
+    const uint8_t* pg = u.e.w_gate + roff;
+    const uint8_t* pu = u.e.w_up + roff;
+    const float* sg = u.e.s_gate + (size_t)(r0 / u.e.gate_rb) * ((H + u.e.gate_cb - 1) / u.e.gate_cb);
+    const float* su = u.e.s_up + (size_t)(r0 / u.e.up_rb) * ((H + u.e.up_cb - 1) / u.e.up_cb);
+    const int kpg = u.e.gate_cb / kKB, kpu = u.e.up_cb / kKB;  // k-blocks per scale column
+
+    const int ntile = (u.np + kTileTok - 1) / kTileTok;
+    const uint16_t* xp[MAXT];
+#pragma unroll
+    for (int tt = 0; tt < MAXT; ++tt) {
+        const int q = min(tt * kTileTok + c, u.np - 1);
+        xp[tt] = static_cast<const uint16_t*>(L.x) + (size_t)pair_token(L, u.pb + q) * H + g * 32;
+    }
+
+    f32x4 accg[MAXT], accu[MAXT];
+#pragma unroll
+    for (int tt = 0; tt < MAXT; ++tt) {
+        accg[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        accu[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    constexpr int D = 4;  // k-blocks in flight per wave
+    u32x4 wb[D][4];
+    u32x4 xb[D][4];
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+        const int k = kb0 + s;
+        if (k < kb1) {
+            wb[s][0] = ld16(pg + k * kKB);
+            wb[s][1] = ld16(pg + k * kKB + 16);
+            wb[s][2] = ld16(pu + k * kKB);
+            wb[s][3] = ld16(pu + k * kKB + 16);
+            if (MAXT == 1) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xb[s][j] = ld16(xp[0] + k * kKB + 8 * j);
+            }
+        }
+    }
+
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    for (int kb = kb0; kb < kb1; kb += D) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) {
+            const int k = kb + s;
+            if (k < kb1) {
+                V ag[4], au[4];
+                ag[0] = M::cvt(wb[s][0][0], wb[s][0][1]);
+                ag[1] = M::cvt(wb[s][0][2], wb[s][0][3]);
+                ag[2] = M::cvt(wb[s][1][0], wb[s][1][1]);
+                ag[3] = M::cvt(wb[s][1][2], wb[s][1][3]);
+                au[0] = M::cvt(wb[s][2][0], wb[s][2][1]);
+                au[1] = M::cvt(wb[s][2][2], wb[s][2][3]);
+                au[2] = M::cvt(wb[s][3][0], wb[s][3][1]);
+                au[3] = M::cvt(wb[s][3][2], wb[s][3][3]);
+                const float scg = sg[k / kpg];
+                const float scu = su[k / kpu];
+#pragma unroll
+                for (int tt = 0; tt < MAXT; ++tt) {
+                    if (tt < ntile) {
+                        V bx[4];
+                        if (MAXT == 1) {
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) bx[j] = M::bits(xb[s][j]);
+                        } else {
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) bx[j] = M::bits(ld16(xp[tt] + k * kKB + 8 * j));
+                        }
+                        f32x4 tg = M::mma(ag[0], bx[0], zero);
+                        f32x4 tu = M::mma(au[0], bx[0], zero);
+#pragma unroll
+                        for (int j = 1; j < 4; ++j) {
+                            tg = M::mma(ag[j], bx[j], tg);
+                            tu = M::mma(au[j], bx[j], tu);
+                        }
+                        accg[tt] += scg * tg;
+                        accu[tt] += scu * tu;
+                    }
+                }
+                const int kn = k + D;
+                if (kn < kb1) {
+                    wb[s][0] = ld16(pg + kn * kKB);
+                    wb[s][1] = ld16(pg + kn * kKB + 16);
+                    wb[s][2] = ld16(pu + kn * kKB);
+                    wb[s][3] = ld16(pu + kn * kKB + 16);
+                    if (MAXT == 1) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) xb[s][j] = ld16(xp[0] + kn * kKB + 8 * j);
+                    }
+                }
+            }
+        }
+    }
+
+    // Cross-wave K reduction in a fixed order, then the SiLU epilogue.
+    __shared__ f32x4 red[kWaves][MAXT][2][64];
+#pragma unroll
+    for (int tt = 0; tt < MAXT; ++tt) {
+        red[wave][tt][0][lane] = accg[tt];
+        red[wave][tt][1][lane] = accu[tt];
+    }
+    __syncthreads();
+    for (int tt = wave; tt < ntile; tt += kWaves) {
+        f32x4 G = red[0][tt][0][lane], U = red[0][tt][1][lane];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) {
+            G += red[w][tt][0][lane];
+            U += red[w][tt][1][lane];
+        }
+        const int q = tt * kTileTok + c;
+        if (q < u.np) {
+            const size_t p = (size_t)(u.pb + q);
+            const int row = r0 + 4 * g;
+            uint32_t hi[4], lo[4];
+            float hv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float gate = G[i], up = U[i];
+                const float silu = gate / (1.0f + expf(-gate));
+                const float h = silu * up;
+                hv[i] = h;
+                hi[i] = bf16_rne(h);
+                lo[i] = bf16_rne(h - __uint_as_float(hi[i] << 16));
+            }
+            uint2 vhi = {hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
+            uint2 vlo = {lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
+            *reinterpret_cast<uint2*>(L.h_hi + p * I + row) = vhi;
+            *reinterpret_cast<uint2*>(L.h_lo + p * I + row) = vlo;
+            if (L.h_f32 != nullptr) {
+                *reinterpret_cast<float4*>(L.h_f32 + p * I + row) =
+                    float4{hv[0], hv[1], hv[2], hv[3]};
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Phase B: down.  Each wave owns 16 rows of Wd (full K = inter), the
+// workgroup 64 rows; B operand = the bf16 hi/lo split of h for <= 16*MAXT
+// pairs.  Writes fp32 per-pair outputs (grouped) or the final output
+// (single mode).  grid = (hidden/64, max_items), block = 256.
+template <int MAXT>
+__global__ __launch_bounds__(256) void k_down(ExpertLaunch L) {
+    typedef Mma<false> M;
+    typedef M::V V;
+    Unit u;
+    if (!resolve_unit(L, kTileTok * MAXT, &u)) return;
+    const int H = u.e.hidden, I = u.e.inter;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int g = lane >> 4, c = lane & 15;
+    const int rw = blockIdx.x * (kTileRows * kWaves) + wave * kTileRows;
+    if (rw >= H) return;
+    const int nkb = I / kKB;
+
+    const uint8_t* pd = u.e.w_down + (size_t)(rw + c) * I + g * 32;
+    const float* sd = u.e.s_down + (size_t)(rw / u.e.down_rb) * ((I + u.e.down_cb - 1) / u.e.down_cb);
+    const int kpd = u.e.down_cb / kKB;
+
+    const int ntile = (u.np + kTileTok - 1) / kTileTok;
+    const uint16_t* hh[MAXT];
+    const uint16_t* hl[MAXT];
+#pragma unroll
+    for (int tt = 0; tt < MAXT; ++tt) {
+        const int q = min(tt * kTileTok + c, u.np - 1);
+        const size_t p = (size_t)(u.pb + q);
+        hh[tt] = L.h_hi + p * I + g * 32;
+        hl[tt] = L.h_lo + p * I + g * 32;
+    }
+
+    f32x4 acc[MAXT];
+#pragma unroll
+    for (int tt = 0; tt < MAXT; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    constexpr int D = 4;
+    u32x4 wb[D][2];
+    u32x4 hb[D][8];
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+        const int k = s;
+        if (k < nkb) {
+            wb[s][0] = ld16(pd + k * kKB);
+            wb[s][1] = ld16(pd + k * kKB + 16);
+            if (MAXT == 1) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    hb[s][j] = ld16(hh[0] + k * kKB + 8 * j);
+                    hb[s][4 + j] = ld16(hl[0] + k * kKB + 8 * j);
+                }
+            }
+        }
+    }
+
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < nkb; kb += D) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) {
+            const int k = kb + s;
+            if (k < nkb) {
+                V a[4];
+                a[0] = M::cvt(wb[s][0][0], wb[s][0][1]);
+                a[1] = M::cvt(wb[s][0][2], wb[s][0][3]);
+                a[2] = M::cvt(wb[s][1][0], wb[s][1][1]);
+                a[3] = M::cvt(wb[s][1][2], wb[s][1][3]);
+                const float sc = sd[k / kpd];
+#pragma unroll
+                for (int tt = 0; tt < MAXT; ++tt) {
+                    if (tt < ntile) {
+                        V bh[4], bl[4];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            if (MAXT == 1) {
+                                bh[j] = M::bits(hb[s][j]);
+                                bl[j] = M::bits(hb[s][4 + j]);
+                            } else {
+                                bh[j] = M::bits(ld16(hh[tt] + k * kKB + 8 * j));
+                                bl[j] = M::bits(ld16(hl[tt] + k * kKB + 8 * j));
+                            }
+                        }
+                        f32x4 t = M::mma(a[0], bh[0], zero);
+                        t = M::mma(a[0], bl[0], t);
+#pragma unroll
+                        for (int j = 1; j < 4; ++j) {
+                            t = M::mma(a[j], bh[j], t);
+                            t = M::mma(a[j], bl[j], t);
+                        }
+                        acc[tt] += sc * t;
+                    }
+                }
+                const int kn = k + D;
+                if (kn < nkb) {
+                    wb[s][0] = ld16(pd + kn * kKB);
+                    wb[s][1] = ld16(pd + kn * kKB + 16);
+                    if (MAXT == 1) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            hb[s][j] = ld16(hh[0] + kn * kKB + 8 * j);
+                            hb[s][4 + j] = ld16(hl[0] + kn * kKB + 8 * j);
+                        }
+                    }
+                }
+            }
+        }
+    }
+
+    const int row = rw + 4 * g;
+#pragma unroll
+    for (int tt = 0; tt < MAXT; ++tt) {
+        const int q = tt * kTileTok + c;
+        if (tt < ntile && q < u.np) {
+            const size_t p = (size_t)(u.pb + q);
+            const f32x4 v = acc[tt];
+            if (L.table != nullptr) {
+                *reinterpret_cast<float4*>(L.y_part + p * H + row) = float4{v[0], v[1], v[2], v[3]};
+            } else {
+                // single mode: pair == token
+                uint16_t* yo = static_cast<uint16_t*>(L.y) + p * H + row;
+                const uint2 o = {cast_out(v[0], L.out_dtype) | (cast_out(v[1], L.out_dtype) << 16),
+                                 cast_out(v[2], L.out_dtype) | (cast_out(v[3], L.out_dtype) << 16)};
+                *reinterpret_cast<uint2*>(yo) = o;
+                if (L.y_f32 != nullptr) {
+                    *reinterpret_cast<float4*>(L.y_f32 + p * H + row) = float4{v[0], v[1], v[2], v[3]};
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Combine: y[t] = sum_k w_k * y_part[pair(t,k)]  (route order, fp32)
+//               + y_part[pair(t, shared)]
+// then cast (RNE).  One thread per 4 consecutive features.
+__global__ __launch_bounds__(256) void k_combine(PlanPtrs plan, const float* __restrict__ y_part,
+                                                 int n_tokens, int top_k, int hidden, void* y,
+                                                 int out_dtype, float* y_f32) {
+    const int n4 = hidden / 4;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n_tokens * n4) return;
+    const int t = idx / n4;
+    const int f = (idx - t * n4) * 4;
+    const int* tp = plan.token_pairs + (size_t)t * (top_k + 1);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < top_k; ++k) {
+        const int p = tp[k];
+        if (p >= 0) {
+            const float w = plan.pair_weight[p];
+            const float4 v = *reinterpret_cast<const float4*>(y_part + (size_t)p * hidden + f);
+            acc[0] += w * v.x;
+            acc[1] += w * v.y;
+            acc[2] += w * v.z;
+            acc[3] += w * v.w;
+        }
+    }
+    const int ps = tp[top_k];
+    if (ps >= 0) {
+        const float4 v = *reinterpret_cast<const float4*>(y_part + (size_t)ps * hidden + f);
+        acc[0] += v.x;
+        acc[1] += v.y;
+        acc[2] += v.z;
+        acc[3] += v.w;
+    }
+    uint16_t* yo = static_cast<uint16_t*>(y) + (size_t)t * hidden + f;
+    const uint2 o = {cast_out(acc[0], out_dtype) | (cast_out(acc[1], out_dtype) << 16),
+                     cast_out(acc[2], out_dtype) | (cast_out(acc[3], out_dtype) << 16)};
+    *reinterpret_cast<uint2*>(yo) = o;
+    if (y_f32 != nullptr) {
+        *reinterpret_cast<float4*>(y_f32 + (size_t)t * hidden + f) = float4{acc[0], acc[1], acc[2], acc[3]};
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Generic single-expert path (any shape / block size): one thread per output
+// row, reference order.  Used for shapes the grouped kernels do not tile
+// (e.g. the 4x8 / 1x1-block experts of the reference's control tests).
+__device__ __forceinline__ float fp8_val(uint8_t b) {
+    return __builtin_amdgcn_cvt_f32_fp8(static_cast<int>(b), 0);
+}
+
+__device__ __forceinline__ float act_val(const void* x, size_t i, int dtype) {
+    const uint16_t b = static_cast<const uint16_t*>(x)[i];
+    if (dtype == CX_DTYPE_FP16) return static_cast<float>(__builtin_bit_cast(_Float16, b));
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+__global__ void k_generic_gate_up(cx_expert_desc e, const void* x, int in_dtype, int n_tokens,
+                                  float* h) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n_tokens * e.inter) return;
+    const int t = idx / e.inter, r = idx - t * e.inter;
+    const int ncu = (e.hidden + e.up_cb - 1) / e.up_cb, ncg = (e.hidden + e.gate_cb - 1) / e.gate_cb;
+    float up = 0.f, gate = 0.f;
+    for (int k = 0; k < e.hidden; ++k) {
+        const float xv = act_val(x, (size_t)t * e.hidden + k, in_dtype);
+        const size_t wi = (size_t)r * e.hidden + k;
+        const float wu = fp8_val(e.w_up[wi]) * e.s_up[(r / e.up_rb) * ncu + k / e.up_cb];
+        const float wg = fp8_val(e.w_gate[wi]) * e.s_gate[(r / e.gate_rb) * ncg + k / e.gate_cb];
+        up = __fadd_rn(up, __fmul_rn(wu, xv));
+        gate = __fadd_rn(gate, __fmul_rn(wg, xv));
+    }
+    h[idx] = (gate / (1.0f + expf(-gate))) * up;
+}
+
+__global__ void k_generic_down(cx_expert_desc e, const float* h, int n_tokens, void* y,
+                               int out_dtype, float* y_f32) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n_tokens * e.hidden) return;
+    const int t = idx / e.hidden, r = idx - t * e.hidden;
+    const int ncd = (e.inter + e.down_cb - 1) / e.down_cb;
+    float sum = 0.f;
+    for (int k = 0; k < e.inter; ++k) {
+        const float w = fp8_val(e.w_down[(size_t)r * e.inter + k]) *
+                        e.s_down[(r / e.down_rb) * ncd + k / e.down_cb];
+        sum = __fadd_rn(sum, __fmul_rn(w, h[(size_t)t * e.inter + k]));
+    }
+    static_cast<uint16_t*>(y)[idx] = static_cast<uint16_t>(cast_out(sum, out_dtype));
+    if (y_f32 != nullptr) y_f32[idx] = sum;
+}
+
+}  // namespace
+
+bool fast_path_ok(const cx_expert_desc& e) {
+    if (e.hidden <= 0 || e.inter <= 0) return false;
+    if (e.hidden % (kTileRows * kWaves) != 0 || e.hidden % kKB != 0) return false;
+    if (e.inter % kKB != 0 || e.hidden / kKB < kWaves) return false;
+    const int rbs[3] = {e.up_rb, e.gate_rb, e.down_rb};
+    const int cbs[3] = {e.up_cb, e.gate_cb, e.down_cb};
+    for (int i = 0; i < 3; ++i) {
+        if (rbs[i] <= 0 || cbs[i] <= 0) return false;
+        if (rbs[i] % kTileRows != 0 || cbs[i] % kKB != 0) return false;
+    }
+    return true;
+}
+
+hipError_t launch_gate_up(const ExpertLaunch& L, hipStream_t s) {
+    const int items = L.table != nullptr ? L.max_items
+                                         : (L.n_tokens + kTileTok * L.maxt - 1) / (kTileTok * L.maxt);
+    const dim3 grid(L.inter / kTileRows, items);
+    const bool f16 = L.in_dtype == CX_DTYPE_FP16;
+    if (L.maxt == 1) {
+        if (f16) hipLaunchKernelGGL((k_gate_up<1, true>), grid, dim3(256), 0, s, L);
+        else hipLaunchKernelGGL((k_gate_up<1, false>), grid, dim3(256), 0, s, L);
+    } else {
+        if (f16) hipLaunchKernelGGL((k_gate_up<4, true>), grid, dim3(256), 0, s, L);
+        else hipLaunchKernelGGL((k_gate_up<4, false>), grid, dim3(256), 0, s, L);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_down(const ExpertLaunch& L, hipStream_t s) {
+    const int items = L.table != nullptr ? L.max_items
+                                         : (L.n_tokens + kTileTok * L.maxt - 1) / (kTileTok * L.maxt);
+    const dim3 grid(L.hidden / (kTileRows * kWaves), items);
+    if (L.maxt == 1) hipLaunchKernelGGL((k_down<1>), grid, dim3(256), 0, s, L);
+    else hipLaunchKernelGGL((k_down<4>), grid, dim3(256), 0, s, L);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine(const PlanPtrs& plan, const float* y_part, int n_tokens, int top_k,
+                          int hidden, void* y, int out_dtype, float* y_f32, hipStream_t s) {
+    const int n = n_tokens * (hidden / 4);
+    hipLaunchKernelGGL(k_combine, dim3((n + 255) / 256), dim3(256), 0, s, plan, y_part,
+                       n_tokens, top_k, hidden, y, out_dtype, y_f32);
+    return hipGetLastError();
+}
+
+hipError_t launch_generic_expert(const cx_expert_desc& e, const void* x, int in_dtype,
+                                 int n_tokens, float* h_scratch, void* y, int out_dtype,
+                                 float* y_f32, hipStream_t s) {
+    const int n1 = n_tokens * e.inter, n2 = n_tokens * e.hidden;
+    hipLaunchKernelGGL(k_generic_gate_up, dim3((n1 + 127) / 128), dim3(128), 0, s, e, x,
+                       in_dtype, n_tokens, h_scratch);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(k_generic_down, dim3((n2 + 127) / 128), dim3(128), 0, s, e, h_scratch,
+                       n_tokens, y, out_dtype, y_f32);
+    return hipGetLastError();
+}
+
+}  // namespace cx

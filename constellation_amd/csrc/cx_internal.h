@@ -1,0 +1,116 @@
+// cx_internal.h — shared declarations of the gfx950 MoE engine (not part of
+// the public ABI; include/cx_moe.h is).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "cx_moe.h"
+
+namespace cx {
+
+// ---------------------------------------------------------------------------
+// Vector types for the gfx950 builtins.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Geometry of the fast grouped kernels.
+constexpr int kKB = 128;        // k-block: one scale per 128 columns
+constexpr int kTileRows = 16;   // MFMA 16x16x32: 16 weight rows per wave
+constexpr int kTileTok = 16;    // 16 token (pair) columns per MFMA tile
+constexpr int kWaves = 4;       // waves per workgroup
+
+// ---------------------------------------------------------------------------
+// Grouped-execution plan, built on the device by k_plan from (topk_ids,
+// topk_w) and consumed by the gate/up, down and combine kernels.
+//   slot   : one active expert (ascending expert id), the shared expert last
+//   pair   : one (token, expert) assignment, grouped by slot
+//   item   : a run of <= item_cap pairs of one slot (one grouped work unit)
+struct PlanHdr {
+    int n_slots;
+    int n_items;
+    int n_pairs;
+    int pad;
+};
+
+struct PlanPtrs {
+    PlanHdr* hdr;
+    int* slot_expert;      // [max_slots]  index into the layer table
+    int* slot_pair_begin;  // [max_slots]
+    int* slot_pair_count;  // [max_slots]
+    int* item_slot;        // [max_items]
+    int* item_pair_begin;  // [max_items]
+    int* item_pair_count;  // [max_items]
+    int* pair_token;       // [max_pairs]
+    float* pair_weight;    // [max_pairs]
+    int* token_pairs;      // [T * (K+1)], pair index or -1 (shared in column K)
+};
+
+// Device error bits (ORed into the context's flag, read by cx_ctx_sync).
+enum : int {
+    kErrBadExpertId = 1,
+    kErrNotResident = 2,
+    kErrPlanOverflow = 4,
+};
+
+// ---------------------------------------------------------------------------
+// Launchers (defined in the .hip files).  All return hipError_t of the launch.
+
+struct ExpertLaunch {
+    // Either a device table + plan (grouped mode) or one descriptor by value
+    // with an implicit identity plan over n_tokens tokens (single mode).
+    const cx_expert_desc* table;  // grouped mode; nullptr in single mode
+    cx_expert_desc single;        // single mode
+    PlanPtrs plan;                // grouped mode
+    int max_items;                // grid bound in grouped mode
+    int n_tokens;
+    int hidden, inter;
+    int maxt;                     // token tiles per item: 1 (decode) or 4 (prefill)
+    const void* x;                // [T, hidden] fp16/bf16
+    int in_dtype;
+    uint16_t* h_hi;               // [pairs, inter] bf16 hi part of h
+    uint16_t* h_lo;               // [pairs, inter] bf16 lo part of h
+    float* h_f32;                 // optional [pairs, inter] fp32 h (debug/parity)
+    float* y_part;                // [pairs, hidden] fp32 per-pair down output (grouped)
+    void* y;                      // single mode: [T, hidden] out dtype
+    float* y_f32;                 // single mode: optional fp32 output
+    int out_dtype;
+};
+
+hipError_t launch_gate_up(const ExpertLaunch& L, hipStream_t s);
+hipError_t launch_down(const ExpertLaunch& L, hipStream_t s);
+hipError_t launch_combine(const PlanPtrs& plan, const float* y_part, int n_tokens,
+                          int top_k, int hidden, void* y, int out_dtype, float* y_f32,
+                          hipStream_t s);
+hipError_t launch_plan(const int32_t* ids, const float* w, int n_tokens, int top_k,
+                       const cx_expert_desc* table, int n_experts, int has_shared,
+                       int item_cap, int max_items, PlanPtrs plan, int* err_flag,
+                       hipStream_t s);
+
+// Generic (any shape, any block size) single-expert path: correctness only.
+hipError_t launch_generic_expert(const cx_expert_desc& e, const void* x, int in_dtype,
+                                 int n_tokens, float* h_scratch, void* y, int out_dtype,
+                                 float* y_f32, hipStream_t s);
+
+// Router.
+hipError_t launch_route(const void* x, int x_dtype, const void* w, int w_dtype,
+                        const float* bias, const uint8_t* resident, int n_tokens,
+                        int hidden, int n_experts, int n_group, int topk_group, int top_k,
+                        int norm, float scale, double* logits, int32_t* ids, float* wout,
+                        hipStream_t s);
+
+// Upload helpers / generator.
+hipError_t launch_canonicalize_fp8(uint8_t* p, uint64_t n, hipStream_t s);
+hipError_t launch_gen_fp8(uint64_t seed, uint64_t stream_id, int rows, int cols, int rb,
+                          int cb, float std_dev, uint8_t* q, float* scale, hipStream_t s);
+hipError_t launch_gen_normal(uint64_t seed, uint64_t stream_id, uint64_t count,
+                             float std_dev, int dtype, void* out, hipStream_t s);
+
+bool fast_path_ok(const cx_expert_desc& e);
+
+}  // namespace cx

@@ -1,0 +1,817 @@
+// cx_runtime.hip — host side of the C ABI (include/cx_moe.h): per-device HBM
+// arena, per-worker contexts with persistent scratch, argument checking,
+// kernel sequencing.  No exceptions cross the ABI; every entry returns an
+// int status and leaves a thread-local message for cx_last_error().
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "cx_internal.h"
+
+using namespace cx;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define CX_HIP(call)                                                                   \
+    do {                                                                               \
+        hipError_t e_ = (call);                                                        \
+        if (e_ != hipSuccess)                                                          \
+            return fail(CX_EHIP, "%s failed: %s", #call, hipGetErrorString(e_));       \
+    } while (0)
+
+int set_device(int device) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n)
+        return fail(CX_EINVAL, "invalid device %d (count %d)", device, n);
+    CX_HIP(hipSetDevice(device));
+    return CX_OK;
+}
+
+size_t act_size(int dtype) { return dtype == CX_DTYPE_F32 ? 4 : 2; }
+bool act16(int dtype) { return dtype == CX_DTYPE_FP16 || dtype == CX_DTYPE_BF16; }
+
+// ---------------------------------------------------------------------------
+// Per-device HBM arena: large hipMalloc chunks, first-fit sub-allocation with
+// coalescing free lists.  Expert weights (44 MB each at DeepSeek shapes) sit
+// back to back in 2 GiB chunks instead of six hipMallocs per expert.
+constexpr size_t kAlign = 256;
+
+struct Chunk {
+    char* base = nullptr;
+    size_t size = 0;
+    std::map<size_t, size_t> free_ranges;  // offset -> length
+};
+
+struct Arena {
+    std::mutex mu;
+    std::vector<Chunk> chunks;
+    std::unordered_map<void*, std::pair<size_t, size_t>> live;  // ptr -> (chunk, len)
+    size_t used = 0, reserved = 0;
+};
+
+Arena& arena(int device) {
+    static Arena arenas[64];
+    return arenas[device & 63];
+}
+
+size_t chunk_bytes() {
+    static size_t v = [] {
+        const char* s = std::getenv("CX_ARENA_CHUNK_MB");
+        size_t mb = s ? std::strtoull(s, nullptr, 10) : 2048;
+        if (mb < 64) mb = 64;
+        return mb << 20;
+    }();
+    return v;
+}
+
+int arena_alloc(int device, size_t bytes, void** out) {
+    *out = nullptr;
+    if (bytes == 0) bytes = kAlign;
+    bytes = (bytes + kAlign - 1) / kAlign * kAlign;
+    Arena& A = arena(device);
+    std::lock_guard<std::mutex> lk(A.mu);
+    for (size_t ci = 0; ci < A.chunks.size(); ++ci) {
+        Chunk& ch = A.chunks[ci];
+        for (auto it = ch.free_ranges.begin(); it != ch.free_ranges.end(); ++it) {
+            if (it->second >= bytes) {
+                const size_t off = it->first, len = it->second;
+                ch.free_ranges.erase(it);
+                if (len > bytes) ch.free_ranges[off + bytes] = len - bytes;
+                void* p = ch.base + off;
+                A.live[p] = {ci, bytes};
+                A.used += bytes;
+                *out = p;
+                return CX_OK;
+            }
+        }
+    }
+    const size_t cb = std::max(chunk_bytes(), (bytes + (2u << 20) - 1) / (2u << 20) * (2u << 20));
+    void* base = nullptr;
+    if (hipMalloc(&base, cb) != hipSuccess || base == nullptr) {
+        (void)hipGetLastError();
+        return fail(CX_ENOMEM, "HBM arena: hipMalloc(%zu) failed (used %zu reserved %zu)", cb,
+                    A.used, A.reserved);
+    }
+    Chunk ch;
+    ch.base = static_cast<char*>(base);
+    ch.size = cb;
+    if (cb > bytes) ch.free_ranges[bytes] = cb - bytes;
+    A.chunks.push_back(std::move(ch));
+    A.reserved += cb;
+    A.live[base] = {A.chunks.size() - 1, bytes};
+    A.used += bytes;
+    *out = base;
+    return CX_OK;
+}
+
+int arena_free(int device, void* p) {
+    if (p == nullptr) return CX_OK;
+    Arena& A = arena(device);
+    std::lock_guard<std::mutex> lk(A.mu);
+    auto it = A.live.find(p);
+    if (it == A.live.end()) return fail(CX_EINVAL, "cx_free_device: %p not allocated here", p);
+    const size_t ci = it->second.first, len = it->second.second;
+    A.live.erase(it);
+    A.used -= len;
+    Chunk& ch = A.chunks[ci];
+    size_t off = static_cast<size_t>(static_cast<char*>(p) - ch.base);
+    size_t l = len;
+    auto nx = ch.free_ranges.lower_bound(off);
+    if (nx != ch.free_ranges.end() && nx->first == off + l) {
+        l += nx->second;
+        ch.free_ranges.erase(nx);
+    }
+    auto pv = ch.free_ranges.lower_bound(off);
+    if (pv != ch.free_ranges.begin()) {
+        --pv;
+        if (pv->first + pv->second == off) {
+            off = pv->first;
+            l += pv->second;
+            ch.free_ranges.erase(pv);
+        }
+    }
+    ch.free_ranges[off] = l;
+    return CX_OK;
+}
+
+hipStream_t upload_stream(int device) {
+    static std::mutex mu;
+    static hipStream_t streams[64] = {};
+    std::lock_guard<std::mutex> lk(mu);
+    if (streams[device & 63] == nullptr) {
+        (void)hipStreamCreateWithFlags(&streams[device & 63], hipStreamNonBlocking);
+    }
+    return streams[device & 63];
+}
+
+// ---------------------------------------------------------------------------
+// Growable device buffer owned by a context.
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+};
+
+int ensure(DevBuf* b, size_t bytes, hipStream_t s) {
+    if (b->bytes >= bytes && b->p != nullptr) return CX_OK;
+    if (b->p != nullptr) {
+        CX_HIP(hipStreamSynchronize(s));
+        CX_HIP(hipFree(b->p));
+        b->p = nullptr;
+        b->bytes = 0;
+    }
+    const size_t want = std::max<size_t>(bytes, 4096);
+    if (hipMalloc(&b->p, want) != hipSuccess) {
+        (void)hipGetLastError();
+        b->p = nullptr;
+        return fail(CX_ENOMEM, "context scratch: hipMalloc(%zu) failed", want);
+    }
+    b->bytes = want;
+    return CX_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+struct cx_ctx {
+    int device = -1;
+    hipStream_t own_stream = nullptr;  // for the host-buffer entry point
+    int* err_flag = nullptr;           // device int
+    DevBuf plan_buf, hhi, hlo, ypart, logits, route_ids, route_w, hscratch;
+    DevBuf dx, dy;                     // cx_expert_run_host staging (device)
+    void* pin_x = nullptr;             // pinned host staging
+    void* pin_y = nullptr;
+    size_t pin_x_bytes = 0, pin_y_bytes = 0;
+    // per-kernel HIP-event timing (cx_ctx_profile)
+    bool prof = false;
+    std::map<std::string, std::vector<std::pair<hipEvent_t, hipEvent_t>>> spans;
+    std::map<std::string, std::pair<int, double>> totals;
+};
+
+struct cx_layer {
+    int n_experts = 0;
+    int has_shared = 0;
+    int fast = 1;                      // every resident expert fits the grouped kernels
+    int hidden = 0, inter = 0;
+    cx_expert_desc* table = nullptr;   // device [n_experts + 1], entry n_experts = shared
+};
+
+namespace {
+
+// Records start/end events around one kernel launch when profiling is on.
+class Span {
+public:
+    Span(cx_ctx* ctx, const char* name, hipStream_t s) : ctx_(ctx), s_(s) {
+        if (!ctx_->prof) return;
+        if (hipEventCreate(&a_) != hipSuccess || hipEventCreate(&b_) != hipSuccess) {
+            (void)hipGetLastError();
+            a_ = b_ = nullptr;
+            return;
+        }
+        (void)hipEventRecord(a_, s_);
+        name_ = name;
+    }
+    ~Span() {
+        if (a_ == nullptr) return;
+        (void)hipEventRecord(b_, s_);
+        ctx_->spans[name_].push_back({a_, b_});
+    }
+
+private:
+    cx_ctx* ctx_;
+    hipStream_t s_;
+    hipEvent_t a_ = nullptr, b_ = nullptr;
+    std::string name_;
+};
+
+void drain_spans(cx_ctx* ctx) {
+    for (auto& kv : ctx->spans) {
+        auto& tot = ctx->totals[kv.first];
+        for (auto& ab : kv.second) {
+            float ms = 0.f;
+            if (hipEventSynchronize(ab.second) == hipSuccess &&
+                hipEventElapsedTime(&ms, ab.first, ab.second) == hipSuccess) {
+                tot.first += 1;
+                tot.second += ms;
+            }
+            (void)hipEventDestroy(ab.first);
+            (void)hipEventDestroy(ab.second);
+        }
+        kv.second.clear();
+    }
+}
+
+struct PlanSizes {
+    int max_slots, max_pairs, max_items, item_cap, maxt;
+};
+
+PlanSizes plan_sizes(int n_tokens, int top_k, int n_experts, int has_shared, bool prefill) {
+    PlanSizes z;
+    z.maxt = (!prefill && n_tokens <= kTileTok) || n_tokens <= kTileTok ? 1 : 4;
+    z.item_cap = kTileTok * z.maxt;
+    z.max_slots = std::min(n_tokens * top_k, n_experts) + has_shared;
+    z.max_pairs = n_tokens * top_k + n_tokens * has_shared;
+    z.max_items = z.max_slots + (z.max_pairs + z.item_cap - 1) / z.item_cap;
+    return z;
+}
+
+int carve_plan(cx_ctx* ctx, const PlanSizes& z, int n_tokens, int top_k, hipStream_t s,
+               PlanPtrs* P) {
+    const size_t ints = 4 + 3 * (size_t)z.max_slots + 3 * (size_t)z.max_items +
+                        2 * (size_t)z.max_pairs + (size_t)n_tokens * (top_k + 1);
+    int rc = ensure(&ctx->plan_buf, ints * 4 + 256, s);
+    if (rc) return rc;
+    int* base = static_cast<int*>(ctx->plan_buf.p);
+    P->hdr = reinterpret_cast<PlanHdr*>(base);
+    int* q = base + 4;
+    P->slot_expert = q; q += z.max_slots;
+    P->slot_pair_begin = q; q += z.max_slots;
+    P->slot_pair_count = q; q += z.max_slots;
+    P->item_slot = q; q += z.max_items;
+    P->item_pair_begin = q; q += z.max_items;
+    P->item_pair_count = q; q += z.max_items;
+    P->pair_token = q; q += z.max_pairs;
+    P->pair_weight = reinterpret_cast<float*>(q); q += z.max_pairs;
+    P->token_pairs = q;
+    return CX_OK;
+}
+
+int check_desc(const cx_expert_desc* e) {
+    if (e == nullptr) return fail(CX_EINVAL, "expert descriptor is NULL");
+    if (!e->w_up || !e->w_gate || !e->w_down || !e->s_up || !e->s_gate || !e->s_down)
+        return fail(CX_EINVAL, "expert descriptor has a NULL buffer");
+    if (e->hidden <= 0 || e->inter <= 0) return fail(CX_EINVAL, "expert dims must be > 0");
+    const int b[6] = {e->up_rb, e->up_cb, e->gate_rb, e->gate_cb, e->down_rb, e->down_cb};
+    for (int v : b)
+        if (v <= 0) return fail(CX_EINVAL, "expert block sizes must be > 0");
+    return CX_OK;
+}
+
+int moe_forward(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int n_tokens,
+                const int32_t* ids, const float* w, int top_k, void* y, int out_dtype,
+                float* y_f32, hipStream_t s, bool prefill) {
+    if (!ctx || !layer) return fail(CX_EINVAL, "NULL context or layer");
+    if (!act16(in_dtype) || !act16(out_dtype)) return fail(CX_EINVAL, "dtypes must be fp16/bf16");
+    if (n_tokens <= 0 || top_k < 0 || top_k > 64) return fail(CX_EINVAL, "bad n_tokens/top_k");
+    if (!x || !y || (top_k > 0 && (!ids || !w))) return fail(CX_EINVAL, "NULL buffer");
+    if (!layer->fast)
+        return fail(CX_EUNSUPPORTED, "layer experts do not fit the grouped kernels "
+                                     "(need hidden%%64==0, dims%%128==0, blocks 16x128 multiples)");
+    int rc = set_device(ctx->device);
+    if (rc) return rc;
+    const PlanSizes z = plan_sizes(n_tokens, top_k, layer->n_experts, layer->has_shared, prefill);
+    if (z.max_pairs == 0) return fail(CX_EINVAL, "nothing to compute");
+    PlanPtrs P;
+    if ((rc = carve_plan(ctx, z, n_tokens, top_k, s, &P))) return rc;
+    const size_t H = layer->hidden, I = layer->inter;
+    if ((rc = ensure(&ctx->hhi, (size_t)z.max_pairs * I * 2, s))) return rc;
+    if ((rc = ensure(&ctx->hlo, (size_t)z.max_pairs * I * 2, s))) return rc;
+    if ((rc = ensure(&ctx->ypart, (size_t)z.max_pairs * H * 4, s))) return rc;
+    {
+        Span sp(ctx, "plan", s);
+        CX_HIP(launch_plan(ids, w, n_tokens, top_k, layer->table, layer->n_experts,
+                           layer->has_shared, z.item_cap, z.max_items, P, ctx->err_flag, s));
+    }
+    ExpertLaunch L{};
+    L.table = layer->table;
+    L.plan = P;
+    L.max_items = z.max_items;
+    L.n_tokens = n_tokens;
+    L.hidden = layer->hidden;
+    L.inter = layer->inter;
+    L.maxt = z.maxt;
+    L.x = x;
+    L.in_dtype = in_dtype;
+    L.h_hi = static_cast<uint16_t*>(ctx->hhi.p);
+    L.h_lo = static_cast<uint16_t*>(ctx->hlo.p);
+    L.y_part = static_cast<float*>(ctx->ypart.p);
+    L.out_dtype = out_dtype;
+    {
+        Span sp(ctx, "gate_up", s);
+        CX_HIP(launch_gate_up(L, s));
+    }
+    {
+        Span sp(ctx, "down", s);
+        CX_HIP(launch_down(L, s));
+    }
+    {
+        Span sp(ctx, "combine", s);
+        CX_HIP(launch_combine(P, L.y_part, n_tokens, top_k, layer->hidden, y, out_dtype, y_f32, s));
+    }
+    return CX_OK;
+}
+
+}  // namespace
+
+// ===========================================================================
+extern "C" {
+
+const char* cx_last_error(void) { return g_err.c_str(); }
+const char* cx_version(void) { return "constellation_amd cx_moe 0.1 (gfx950)"; }
+
+int cx_device_count(int* count) {
+    if (!count) return fail(CX_EINVAL, "NULL count");
+    *count = 0;
+    CX_HIP(hipGetDeviceCount(count));
+    return CX_OK;
+}
+
+int cx_device_query(int device, cx_device_info* out) {
+    if (!out) return fail(CX_EINVAL, "NULL out");
+    std::memset(out, 0, sizeof(*out));
+    int rc = set_device(device);
+    if (rc) return rc;
+    hipDeviceProp_t prop;
+    CX_HIP(hipGetDeviceProperties(&prop, device));
+    std::snprintf(out->name, sizeof(out->name), "%s", prop.name);
+    std::snprintf(out->arch, sizeof(out->arch), "%s", prop.gcnArchName);
+    out->total_mem_bytes = prop.totalGlobalMem;
+    size_t fr = 0, tot = 0;
+    CX_HIP(hipMemGetInfo(&fr, &tot));
+    out->free_mem_bytes = fr;
+    out->compute_units = prop.multiProcessorCount;
+    uint32_t caps = 1u | 2u;  // kGpuCapFp16 | kGpuCapBf16 (common/types.h:76-77)
+    if (std::strncmp(prop.gcnArchName, "gfx95", 5) == 0 || std::strncmp(prop.gcnArchName, "gfx94", 5) == 0)
+        caps |= 4u;           // kGpuCapFp8
+    out->capability_flags = caps;
+    int xcc = 0;
+    if (hipDeviceGetAttribute(&xcc, hipDeviceAttributeNumberOfXccs, device) != hipSuccess) {
+        (void)hipGetLastError();
+        xcc = 0;
+    }
+    out->num_xcds = xcc;
+    return CX_OK;
+}
+
+int cx_upload_matrix(int device, const uint8_t* host_weight, uint64_t rows, uint64_t cols,
+                     const float* host_scale, uint64_t scale_count, uint8_t** dev_weight,
+                     float** dev_scale) {
+    if (!dev_weight || !dev_scale) return fail(CX_EINVAL, "NULL output pointer");
+    *dev_weight = nullptr;
+    *dev_scale = nullptr;
+    if (!host_weight || !host_scale || rows == 0 || cols == 0 || scale_count == 0)
+        return fail(CX_EINVAL, "empty matrix or scales");
+    int rc = set_device(device);
+    if (rc) return rc;
+    const size_t wbytes = rows * cols, sbytes = scale_count * 4;
+    void *pw = nullptr, *ps = nullptr;
+    if ((rc = arena_alloc(device, wbytes, &pw))) return rc;
+    if ((rc = arena_alloc(device, sbytes, &ps))) {
+        arena_free(device, pw);
+        return rc;
+    }
+    hipStream_t s = upload_stream(device);
+    hipError_t e = hipMemcpyAsync(pw, host_weight, wbytes, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(ps, host_scale, sbytes, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = launch_canonicalize_fp8(static_cast<uint8_t*>(pw), wbytes, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        arena_free(device, pw);
+        arena_free(device, ps);
+        return fail(CX_EHIP, "upload failed: %s", hipGetErrorString(e));
+    }
+    *dev_weight = static_cast<uint8_t*>(pw);
+    *dev_scale = static_cast<float*>(ps);
+    return CX_OK;
+}
+
+int cx_free_device(int device, void* dev_ptr) {
+    if (device < 0 || device >= 64) return fail(CX_EINVAL, "bad device");
+    return arena_free(device, dev_ptr);
+}
+
+int cx_arena_stats(int device, uint64_t* used_bytes, uint64_t* reserved_bytes) {
+    if (device < 0 || device >= 64) return fail(CX_EINVAL, "bad device");
+    Arena& A = arena(device);
+    std::lock_guard<std::mutex> lk(A.mu);
+    if (used_bytes) *used_bytes = A.used;
+    if (reserved_bytes) *reserved_bytes = A.reserved;
+    return CX_OK;
+}
+
+int cx_ctx_create(int device, cx_ctx** out) {
+    if (!out) return fail(CX_EINVAL, "NULL out");
+    *out = nullptr;
+    int rc = set_device(device);
+    if (rc) return rc;
+    cx_ctx* c = new (std::nothrow) cx_ctx();
+    if (!c) return fail(CX_ENOMEM, "out of host memory");
+    c->device = device;
+    if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipMalloc(&c->err_flag, sizeof(int)) != hipSuccess ||
+        hipMemset(c->err_flag, 0, sizeof(int)) != hipSuccess) {
+        cx_ctx_destroy(c);
+        return fail(CX_EHIP, "context init failed");
+    }
+    *out = c;
+    return CX_OK;
+}
+
+int cx_ctx_destroy(cx_ctx* c) {
+    if (!c) return CX_OK;
+    (void)hipSetDevice(c->device);
+    (void)hipDeviceSynchronize();
+    drain_spans(c);
+    DevBuf* bufs[] = {&c->plan_buf, &c->hhi, &c->hlo, &c->ypart, &c->logits, &c->route_ids,
+                      &c->route_w, &c->hscratch, &c->dx, &c->dy};
+    for (DevBuf* b : bufs)
+        if (b->p) (void)hipFree(b->p);
+    if (c->err_flag) (void)hipFree(c->err_flag);
+    if (c->pin_x) (void)hipHostFree(c->pin_x);
+    if (c->pin_y) (void)hipHostFree(c->pin_y);
+    if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
+    delete c;
+    return CX_OK;
+}
+
+int cx_ctx_sync(cx_ctx* ctx, void* stream) {
+    if (!ctx) return fail(CX_EINVAL, "NULL context");
+    int rc = set_device(ctx->device);
+    if (rc) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int flag = 0;
+    CX_HIP(hipMemcpyAsync(&flag, ctx->err_flag, sizeof(int), hipMemcpyDeviceToHost, s));
+    CX_HIP(hipStreamSynchronize(s));
+    if (flag != 0) {
+        CX_HIP(hipMemsetAsync(ctx->err_flag, 0, sizeof(int), s));
+        CX_HIP(hipStreamSynchronize(s));
+        return fail(CX_EDEVICE, "device check failed (flags 0x%x:%s%s%s)", flag,
+                    (flag & kErrBadExpertId) ? " expert id out of range" : "",
+                    (flag & kErrNotResident) ? " expert not resident" : "",
+                    (flag & kErrPlanOverflow) ? " plan overflow" : "");
+    }
+    return CX_OK;
+}
+
+int cx_ctx_profile(cx_ctx* ctx, int enable) {
+    if (!ctx) return fail(CX_EINVAL, "NULL context");
+    int rc = set_device(ctx->device);
+    if (rc) return rc;
+    drain_spans(ctx);
+    if (enable) ctx->totals.clear();
+    ctx->prof = enable != 0;
+    return CX_OK;
+}
+
+int cx_ctx_profile_read(cx_ctx* ctx, const char* kernel, int* launches, double* total_ms) {
+    if (!ctx || !kernel || !launches || !total_ms) return fail(CX_EINVAL, "NULL argument");
+    int rc = set_device(ctx->device);
+    if (rc) return rc;
+    drain_spans(ctx);
+    auto it = ctx->totals.find(kernel);
+    *launches = it == ctx->totals.end() ? 0 : it->second.first;
+    *total_ms = it == ctx->totals.end() ? 0.0 : it->second.second;
+    return CX_OK;
+}
+
+int cx_expert_run(cx_ctx* ctx, const cx_expert_desc* expert, const void* x, int in_dtype,
+                  int n_tokens, void* y, int out_dtype, float* y_f32, void* stream) {
+    if (!ctx) return fail(CX_EINVAL, "NULL context");
+    int rc = check_desc(expert);
+    if (rc) return rc;
+    if (!act16(in_dtype) || !act16(out_dtype)) return fail(CX_EINVAL, "dtypes must be fp16/bf16");
+    if (n_tokens <= 0 || !x || !y) return fail(CX_EINVAL, "bad n_tokens or NULL buffer");
+    if ((rc = set_device(ctx->device))) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t I = expert->inter;
+    if (!fast_path_ok(*expert)) {
+        if ((rc = ensure(&ctx->hscratch, (size_t)n_tokens * I * 4, s))) return rc;
+        CX_HIP(launch_generic_expert(*expert, x, in_dtype, n_tokens,
+                                     static_cast<float*>(ctx->hscratch.p), y, out_dtype, y_f32, s));
+        return CX_OK;
+    }
+    if ((rc = ensure(&ctx->hhi, (size_t)n_tokens * I * 2, s))) return rc;
+    if ((rc = ensure(&ctx->hlo, (size_t)n_tokens * I * 2, s))) return rc;
+    ExpertLaunch L{};
+    L.table = nullptr;
+    L.single = *expert;
+    L.n_tokens = n_tokens;
+    L.hidden = expert->hidden;
+    L.inter = expert->inter;
+    L.maxt = n_tokens <= kTileTok ? 1 : 4;
+    L.x = x;
+    L.in_dtype = in_dtype;
+    L.h_hi = static_cast<uint16_t*>(ctx->hhi.p);
+    L.h_lo = static_cast<uint16_t*>(ctx->hlo.p);
+    L.y = y;
+    L.y_f32 = y_f32;
+    L.out_dtype = out_dtype;
+    {
+        Span sp(ctx, "gate_up", s);
+        CX_HIP(launch_gate_up(L, s));
+    }
+    {
+        Span sp(ctx, "down", s);
+        CX_HIP(launch_down(L, s));
+    }
+    return CX_OK;
+}
+
+int cx_expert_run_host(cx_ctx* ctx, const cx_expert_desc* expert, const void* x_host,
+                       size_t x_bytes, int in_dtype, int n_tokens, void* y_host, size_t y_bytes,
+                       int out_dtype) {
+    if (!ctx) return fail(CX_EINVAL, "NULL context");
+    int rc = check_desc(expert);
+    if (rc) return rc;
+    if (!act16(in_dtype) || !act16(out_dtype)) return fail(CX_EINVAL, "dtypes must be fp16/bf16");
+    if (n_tokens <= 0 || !x_host || !y_host) return fail(CX_EINVAL, "bad n_tokens or NULL buffer");
+    const size_t elems = (size_t)n_tokens * expert->hidden;
+    if (x_bytes != elems * act_size(in_dtype))
+        return fail(CX_EINVAL, "activation bytes %zu != batch*hidden*%zu", x_bytes, act_size(in_dtype));
+    if (y_bytes != elems * act_size(out_dtype))
+        return fail(CX_EINVAL, "output bytes %zu != batch*hidden*%zu", y_bytes, act_size(out_dtype));
+    if ((rc = set_device(ctx->device))) return rc;
+    hipStream_t s = ctx->own_stream;
+    if ((rc = ensure(&ctx->dx, x_bytes, s))) return rc;
+    if ((rc = ensure(&ctx->dy, y_bytes, s))) return rc;
+    if (ctx->pin_x_bytes < x_bytes) {
+        if (ctx->pin_x) (void)hipHostFree(ctx->pin_x);
+        ctx->pin_x = nullptr;
+        ctx->pin_x_bytes = 0;
+        CX_HIP(hipHostMalloc(&ctx->pin_x, x_bytes, hipHostMallocDefault));
+        ctx->pin_x_bytes = x_bytes;
+    }
+    if (ctx->pin_y_bytes < y_bytes) {
+        if (ctx->pin_y) (void)hipHostFree(ctx->pin_y);
+        ctx->pin_y = nullptr;
+        ctx->pin_y_bytes = 0;
+        CX_HIP(hipHostMalloc(&ctx->pin_y, y_bytes, hipHostMallocDefault));
+        ctx->pin_y_bytes = y_bytes;
+    }
+    std::memcpy(ctx->pin_x, x_host, x_bytes);
+    CX_HIP(hipMemcpyAsync(ctx->dx.p, ctx->pin_x, x_bytes, hipMemcpyHostToDevice, s));
+    if ((rc = cx_expert_run(ctx, expert, ctx->dx.p, in_dtype, n_tokens, ctx->dy.p, out_dtype,
+                            nullptr, s)))
+        return rc;
+    CX_HIP(hipMemcpyAsync(ctx->pin_y, ctx->dy.p, y_bytes, hipMemcpyDeviceToHost, s));
+    CX_HIP(hipStreamSynchronize(s));
+    std::memcpy(y_host, ctx->pin_y, y_bytes);
+    return CX_OK;
+}
+
+int cx_layer_create(cx_ctx* ctx, int n_experts, const cx_expert_desc* const* experts,
+                    const cx_expert_desc* shared, cx_layer** out) {
+    if (!ctx || !out) return fail(CX_EINVAL, "NULL argument");
+    *out = nullptr;
+    if (n_experts <= 0 || n_experts > 4096) return fail(CX_EINVAL, "n_experts must be 1..4096");
+    int rc = set_device(ctx->device);
+    if (rc) return rc;
+    std::vector<cx_expert_desc> host(n_experts + 1);
+    std::memset(host.data(), 0, sizeof(cx_expert_desc) * host.size());
+    int H = 0, I = 0, fast = 1, any = 0;
+    auto take = [&](const cx_expert_desc* e, cx_expert_desc* dst) -> int {
+        int r = check_desc(e);
+        if (r) return r;
+        if (any && (e->hidden != H || e->inter != I))
+            return fail(CX_EINVAL, "all experts of a layer must share hidden/inter dims");
+        H = e->hidden;
+        I = e->inter;
+        any = 1;
+        fast &= fast_path_ok(*e) ? 1 : 0;
+        *dst = *e;
+        return CX_OK;
+    };
+    for (int i = 0; i < n_experts; ++i)
+        if (experts && experts[i] && (rc = take(experts[i], &host[i]))) return rc;
+    if (shared && (rc = take(shared, &host[n_experts]))) return rc;
+    if (!any) return fail(CX_EINVAL, "layer has no resident expert");
+    cx_layer* L = new (std::nothrow) cx_layer();
+    if (!L) return fail(CX_ENOMEM, "out of host memory");
+    L->n_experts = n_experts;
+    L->has_shared = shared ? 1 : 0;
+    L->fast = fast;
+    L->hidden = H;
+    L->inter = I;
+    if (hipMalloc(&L->table, sizeof(cx_expert_desc) * host.size()) != hipSuccess ||
+        hipMemcpy(L->table, host.data(), sizeof(cx_expert_desc) * host.size(),
+                  hipMemcpyHostToDevice) != hipSuccess) {
+        if (L->table) (void)hipFree(L->table);
+        delete L;
+        return fail(CX_EHIP, "layer table upload failed");
+    }
+    *out = L;
+    return CX_OK;
+}
+
+int cx_layer_destroy(cx_ctx* ctx, cx_layer* layer) {
+    if (!layer) return CX_OK;
+    if (ctx) (void)hipSetDevice(ctx->device);
+    (void)hipDeviceSynchronize();
+    if (layer->table) (void)hipFree(layer->table);
+    delete layer;
+    return CX_OK;
+}
+
+int cx_route(cx_ctx* ctx, const void* x, int x_dtype, const void* w_router, int w_dtype,
+             const float* bias, const uint8_t* resident, int n_tokens, int hidden, int n_experts,
+             int n_group, int topk_group, int top_k, int norm_topk_prob,
+             float routed_scaling_factor, int32_t* topk_ids, float* topk_w, void* stream) {
+    if (!ctx) return fail(CX_EINVAL, "NULL context");
+    if (!x || !w_router || !bias || !topk_ids || !topk_w) return fail(CX_EINVAL, "NULL buffer");
+    if ((x_dtype != CX_DTYPE_BF16 && x_dtype != CX_DTYPE_F32) ||
+        (w_dtype != CX_DTYPE_BF16 && w_dtype != CX_DTYPE_F32))
+        return fail(CX_EINVAL, "router x / weight dtype must be bf16 or fp32");
+    if (n_tokens <= 0 || hidden <= 0 || hidden % 8 != 0)
+        return fail(CX_EINVAL, "hidden must be a positive multiple of 8");
+    if (n_experts <= 0 || n_experts > 1024) return fail(CX_EINVAL, "n_experts must be 1..1024");
+    if (n_group <= 0 || n_group > 64 || n_experts % n_group != 0)
+        return fail(CX_EINVAL, "n_experts=%d not divisible by n_group=%d", n_experts, n_group);
+    if (topk_group <= 0 || topk_group > n_group)
+        return fail(CX_EINVAL, "invalid topk_group=%d for n_group=%d", topk_group, n_group);
+    if (top_k <= 0 || top_k > n_experts || top_k > 64)
+        return fail(CX_EINVAL, "invalid top_k=%d for num_experts=%d", top_k, n_experts);
+    int rc = set_device(ctx->device);
+    if (rc) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if ((rc = ensure(&ctx->logits, (size_t)n_tokens * n_experts * 8, s))) return rc;
+    Span sp(ctx, "route", s);
+    CX_HIP(launch_route(x, x_dtype, w_router, w_dtype, bias, resident, n_tokens, hidden, n_experts,
+                        n_group, topk_group, top_k, norm_topk_prob, routed_scaling_factor,
+                        static_cast<double*>(ctx->logits.p), topk_ids, topk_w, s));
+    return CX_OK;
+}
+
+int cx_moe_decode(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int n_tokens,
+                  const int32_t* topk_ids, const float* topk_w, int top_k, void* y, int out_dtype,
+                  float* y_f32, void* stream) {
+    return moe_forward(ctx, layer, x, in_dtype, n_tokens, topk_ids, topk_w, top_k, y, out_dtype,
+                       y_f32, static_cast<hipStream_t>(stream), false);
+}
+
+int cx_moe_prefill(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int n_tokens,
+                   const int32_t* topk_ids, const float* topk_w, int top_k, void* y,
+                   int out_dtype, float* y_f32, void* stream) {
+    return moe_forward(ctx, layer, x, in_dtype, n_tokens, topk_ids, topk_w, top_k, y, out_dtype,
+                       y_f32, static_cast<hipStream_t>(stream), true);
+}
+
+int cx_moe_layer(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int n_tokens,
+                 const void* w_router, int w_dtype, const float* bias, const uint8_t* resident,
+                 int n_group, int topk_group, int top_k, int norm_topk_prob,
+                 float routed_scaling_factor, void* y, int out_dtype, float* y_f32,
+                 int32_t* topk_ids, float* topk_w, void* stream) {
+    if (!ctx || !layer) return fail(CX_EINVAL, "NULL context or layer");
+    if (in_dtype != CX_DTYPE_BF16)
+        return fail(CX_EINVAL, "cx_moe_layer routes bf16 activations (in_dtype must be bf16)");
+    int rc = set_device(ctx->device);
+    if (rc) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int32_t* ids = topk_ids;
+    float* w = topk_w;
+    if (!ids) {
+        if ((rc = ensure(&ctx->route_ids, (size_t)n_tokens * top_k * 4, s))) return rc;
+        ids = static_cast<int32_t*>(ctx->route_ids.p);
+    }
+    if (!w) {
+        if ((rc = ensure(&ctx->route_w, (size_t)n_tokens * top_k * 4, s))) return rc;
+        w = static_cast<float*>(ctx->route_w.p);
+    }
+    if ((rc = cx_route(ctx, x, in_dtype, w_router, w_dtype, bias, resident, n_tokens,
+                       layer->hidden, layer->n_experts, n_group, topk_group, top_k, norm_topk_prob,
+                       routed_scaling_factor, ids, w, stream)))
+        return rc;
+    return moe_forward(ctx, layer, x, in_dtype, n_tokens, ids, w, top_k, y, out_dtype, y_f32, s,
+                       n_tokens > kTileTok);
+}
+
+int cx_gen_fp8_matrix(cx_ctx* ctx, uint64_t seed, uint64_t stream_id, int rows, int cols,
+                      int row_block, int col_block, float std_dev, uint8_t* dev_weight,
+                      float* dev_scale, void* stream) {
+    if (!ctx || !dev_weight || !dev_scale) return fail(CX_EINVAL, "NULL argument");
+    if (rows <= 0 || cols <= 0 || row_block <= 0 || col_block <= 0)
+        return fail(CX_EINVAL, "bad matrix geometry");
+    int rc = set_device(ctx->device);
+    if (rc) return rc;
+    CX_HIP(launch_gen_fp8(seed, stream_id, rows, cols, row_block, col_block, std_dev, dev_weight,
+                          dev_scale, static_cast<hipStream_t>(stream)));
+    return CX_OK;
+}
+
+int cx_gen_normal(cx_ctx* ctx, uint64_t seed, uint64_t stream_id, uint64_t count, float std_dev,
+                  int dtype, void* dev_out, void* stream) {
+    if (!ctx || !dev_out) return fail(CX_EINVAL, "NULL argument");
+    if (dtype != CX_DTYPE_F32 && !act16(dtype)) return fail(CX_EINVAL, "bad dtype");
+    int rc = set_device(ctx->device);
+    if (rc) return rc;
+    CX_HIP(launch_gen_normal(seed, stream_id, count, std_dev, dtype, dev_out,
+                             static_cast<hipStream_t>(stream)));
+    return CX_OK;
+}
+
+int cx_gen_expert(int device, uint64_t seed, uint64_t stream_base, int hidden, int inter,
+                  int block, float std_dev, cx_expert_desc* out) {
+    if (!out) return fail(CX_EINVAL, "NULL out");
+    std::memset(out, 0, sizeof(*out));
+    if (hidden <= 0 || inter <= 0 || block <= 0) return fail(CX_EINVAL, "bad expert geometry");
+    int rc = set_device(device);
+    if (rc) return rc;
+    const size_t nsu = (size_t)((inter + block - 1) / block) * ((hidden + block - 1) / block);
+    const size_t nsd = (size_t)((hidden + block - 1) / block) * ((inter + block - 1) / block);
+    void* p[6] = {};
+    const size_t sz[6] = {(size_t)inter * hidden, nsu * 4, (size_t)inter * hidden, nsu * 4,
+                          (size_t)hidden * inter, nsd * 4};
+    for (int i = 0; i < 6; ++i) {
+        if ((rc = arena_alloc(device, sz[i], &p[i]))) {
+            for (int j = 0; j < i; ++j) arena_free(device, p[j]);
+            return rc;
+        }
+    }
+    hipStream_t s = upload_stream(device);
+    hipError_t e = launch_gen_fp8(seed, stream_base + 0, inter, hidden, block, block, std_dev,
+                                  static_cast<uint8_t*>(p[0]), static_cast<float*>(p[1]), s);
+    if (e == hipSuccess)
+        e = launch_gen_fp8(seed, stream_base + 1, inter, hidden, block, block, std_dev,
+                           static_cast<uint8_t*>(p[2]), static_cast<float*>(p[3]), s);
+    if (e == hipSuccess)
+        e = launch_gen_fp8(seed, stream_base + 2, hidden, inter, block, block, std_dev,
+                           static_cast<uint8_t*>(p[4]), static_cast<float*>(p[5]), s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        for (int j = 0; j < 6; ++j) arena_free(device, p[j]);
+        return fail(CX_EHIP, "expert generation failed: %s", hipGetErrorString(e));
+    }
+    out->w_up = static_cast<uint8_t*>(p[0]);
+    out->s_up = static_cast<float*>(p[1]);
+    out->w_gate = static_cast<uint8_t*>(p[2]);
+    out->s_gate = static_cast<float*>(p[3]);
+    out->w_down = static_cast<uint8_t*>(p[4]);
+    out->s_down = static_cast<float*>(p[5]);
+    out->hidden = hidden;
+    out->inter = inter;
+    out->up_rb = out->up_cb = out->gate_rb = out->gate_cb = out->down_rb = out->down_cb = block;
+    return CX_OK;
+}
+
+int cx_free_expert(int device, cx_expert_desc* e) {
+    if (!e) return fail(CX_EINVAL, "NULL expert");
+    const void* p[6] = {e->w_up, e->s_up, e->w_gate, e->s_gate, e->w_down, e->s_down};
+    int rc = CX_OK;
+    for (const void* q : p) {
+        if (q) {
+            const int r = arena_free(device, const_cast<void*>(q));
+            if (r) rc = r;
+        }
+    }
+    std::memset(e, 0, sizeof(*e));
+    return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,169 @@
+"""GPU parity of the single-expert path (cx_expert_run, cx_expert_run_host)
+against the CPU oracle and the reference's golden vectors.
+
+Tolerances: fp32 pre-cast output within rel-L2 <= 1e-2
+and max-abs <= 2e-2 of the dequantise-then-fp32 oracle; the kernels do much
+better, so the tests also assert the tighter bounds they actually meet.
+Reference KAT thresholds (test_benchmark_run_expert_cuda_v2.cc:302-305):
+max_abs <= 5e-3, mean_abs <= 1e-3, cos >= 0.9999 on the 16-bit outputs.
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.oracle import BF16, FP16, dummy_expert_np, expert_f64, rel_l2
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).parent / "golden"
+TDT = {FP16: torch.float16, BF16: torch.bfloat16}
+
+
+def _to_dev_bits(bits: np.ndarray, dt: int) -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(TDT[dt])
+    return t.cuda()
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def _upload(ex):
+    from constellation_amd.engine import Expert
+    return Expert.upload(0, ex["w_up"], ex["s_up"], ex["w_gate"], ex["s_gate"], ex["w_down"],
+                         ex["s_down"], row_block=ex["rb"], col_block=ex["cb"])
+
+
+def _metrics(got, ref):
+    got = np.asarray(got, np.float64).ravel()
+    ref = np.asarray(ref, np.float64).ravel()
+    d = np.abs(got - ref)
+    cos = float(got @ ref / (np.linalg.norm(got) * np.linalg.norm(ref)))
+    return float(d.max()), float(d.mean()), cos
+
+
+@pytest.mark.parametrize("name,dt", [("fp16", FP16), ("bf16", BF16)])
+def test_reference_kat_dummy_bundle(gpu, oracle, name, dt):
+    """The reference's own KAT: dummy bundle (all 256 codes incl. 0x7F/0xFF),
+    x = sin(0.0005 i); compared with RunExpertReferenceV2's output."""
+    print(f"[kat] dtype={name}", flush=True)
+    g = np.load(GOLDEN / "dummy_kat.npz")
+    ex = dummy_expert_np()
+    e = _upload(ex)
+    try:
+        x = _to_dev_bits(g[f"x_{name}"], dt).view(1, -1)
+        y, yf = gpu.expert_run(e, x, want_f32=True)
+        torch.cuda.synchronize()
+        ref = oracle.decode_act(g[f"y_{name}"], dt)
+        got = oracle.decode_act(_bits(y)[0], dt)
+        mx, mean, cos = _metrics(got, ref)
+        if dt == FP16:
+            assert mx <= 5e-3 and mean <= 1e-3 and cos >= 0.9999, (mx, mean, cos)
+        else:
+            # bf16 has 8 significant bits: |y| up to ~8 gives a 0.03 ulp, so the
+            # fp16 thresholds become "at most one ulp apart" here
+            ulp = np.abs(_bits(y)[0].astype(np.int32) - g[f"y_{name}"].astype(np.int32))
+            assert ulp.max() <= 1 and mean <= 1e-3 and cos >= 0.9999, (ulp.max(), mean, cos)
+        # fp32 pre-cast output against float64 exact math
+        _, y64 = expert_f64(ex, oracle.decode_act(g[f"x_{name}"], dt), oracle.fp8_lut)
+        assert rel_l2(yf.cpu().numpy(), y64) < 1e-4
+    finally:
+        e.free()
+
+
+def test_seeded_config0_expert(gpu, oracle):
+    """N(0,0.02) expert quantised per 128x128 block, x~N(0,1) bf16."""
+    print("[config0] seeded expert", flush=True)
+    from constellation_amd.engine import Expert
+    g = np.load(GOLDEN / "seeded_expert.npz")
+    e = Expert.generate(0, int(g["seed"]), int(g["stream_base"]))
+    try:
+        ex = e.download()
+        cpu = oracle.gen_expert(int(g["seed"]), int(g["stream_base"]))
+        for k in ("w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down"):
+            assert np.array_equal(ex[k].view(np.uint8), np.ascontiguousarray(cpu[k]).view(np.uint8)), k
+        x = gpu.gen_normal(int(g["seed"]), int(g["x_stream"]), (1, 7168), 1.0, torch.bfloat16)
+        assert np.array_equal(_bits(x)[0], g["x_bf16"])
+        y, yf = gpu.expert_run(e, x, want_f32=True)
+        torch.cuda.synchronize()
+        xf = oracle.decode_act(g["x_bf16"], BF16)
+        _, yref = oracle.expert_ref(cpu, xf)
+        yf = yf.cpu().numpy()
+        assert rel_l2(yf, yref) <= 1e-2 and np.abs(yf - yref).max() <= 2e-2
+        assert rel_l2(yf, yref) < 1e-5, rel_l2(yf, yref)
+        # bf16 output = RNE of our fp32 output, and within 1 ulp of the reference's
+        assert np.array_equal(_bits(y)[0], oracle.encode_act(yf[0], BF16, "rne"))
+        refb = oracle.decode_act(g["y_bf16"], BF16)
+        gotb = oracle.decode_act(_bits(y)[0], BF16)
+        ulp = np.abs((refb.view(np.int32) - gotb.view(np.int32)))
+        assert ulp.max() <= 1, ulp.max()
+    finally:
+        e.free()
+
+
+@pytest.mark.parametrize("T", [1, 2, 5, 16, 17, 40, 100])
+@pytest.mark.parametrize("in_dt,out_dt", [(BF16, BF16), (FP16, FP16), (BF16, FP16), (FP16, BF16)])
+def test_batched_tokens_small_dims(gpu, oracle, T, in_dt, out_dt):
+    """B >= 1 (the reference requires batch == 1, backend_workspace_cuda_v2.cc:146)."""
+    print(f"[batch] T={T} in={in_dt} out={out_dt}", flush=True)
+    H, I = 1024, 256
+    ex = oracle.gen_expert(77, 0x500, hidden=H, inter=I)
+    e = _upload(ex)
+    try:
+        xb = oracle.gen_normal(78, T, T * H, 1.0, "bf16" if in_dt == BF16 else "fp16").reshape(T, H)
+        x = _to_dev_bits(xb, in_dt)
+        y, yf = gpu.expert_run(e, x, out_dtype=TDT[out_dt], want_f32=True)
+        torch.cuda.synchronize()
+        _, yref = oracle.expert_ref(ex, oracle.decode_act(xb, in_dt))
+        yf = yf.cpu().numpy()
+        assert rel_l2(yf, yref) < 1e-5
+        assert np.array_equal(_bits(y), oracle.encode_act(yf, out_dt, "rne"))
+    finally:
+        e.free()
+
+
+def test_generic_shape_one_by_one_blocks(gpu, oracle):
+    """The reference control tests upload 4x8 experts with 1x1 blocks
+    (server/test/0_control_duplicate_upload_same_slot.py); upload and run must accept them."""
+    print("[generic] 8x4 1x1 blocks", flush=True)
+    rng = np.random.default_rng(9)
+    H, I = 8, 4
+    ex = dict(w_up=rng.integers(0, 256, (I, H), dtype=np.uint8),
+              w_gate=rng.integers(0, 256, (I, H), dtype=np.uint8),
+              w_down=rng.integers(0, 256, (H, I), dtype=np.uint8),
+              s_up=rng.uniform(0.01, 0.02, (I, H)).astype(np.float32),
+              s_gate=rng.uniform(0.01, 0.02, (I, H)).astype(np.float32),
+              s_down=rng.uniform(0.01, 0.02, (H, I)).astype(np.float32),
+              hidden=H, inter=I, rb=1, cb=1)
+    e = _upload(ex)
+    try:
+        xb = oracle.gen_normal(1, 1, 2 * H, 1.0, "bf16").reshape(2, H)
+        y, yf = gpu.expert_run(e, _to_dev_bits(xb, BF16), want_f32=True)
+        torch.cuda.synchronize()
+        _, yref = oracle.expert_ref(ex, oracle.decode_act(xb, BF16))
+        assert rel_l2(yf.cpu().numpy(), yref) < 1e-5
+    finally:
+        e.free()
+
+
+def test_run_host_contract(gpu, oracle):
+    """cx_expert_run_host = BackendWorkspaceV2::RunExpertRequest semantics:
+    host bytes in/out, size checks, fp16 wire dtype."""
+    print("[host] run_host", flush=True)
+    from constellation_amd import CxError
+    H, I = 1024, 256
+    ex = oracle.gen_expert(5, 0x600, hidden=H, inter=I)
+    e = _upload(ex)
+    try:
+        xb = oracle.gen_normal(6, 1, 3 * H, 1.0, "fp16")
+        out = gpu.expert_run_host(e, xb.tobytes(), FP16, 3, FP16)
+        got = np.frombuffer(out, np.uint16).reshape(3, H)
+        _, yref = oracle.expert_ref(ex, oracle.decode_act(xb.reshape(3, H), FP16))
+        assert rel_l2(oracle.decode_act(got, FP16), yref) < 1e-3
+        with pytest.raises(CxError):
+            gpu.expert_run_host(e, xb.tobytes()[:-2], FP16, 3, FP16)
+    finally:
+        e.free()
