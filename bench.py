@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
-"""MoE-layer decode benchmark on one MI355X (BASELINE.json metric).
+"""MoE-layer decode benchmark on one MI355X: us/token and achieved HBM GB/s.
 
-Workload (BASELINE config 1): one DeepSeek-V3 MoE layer at decode batch 1 —
+Workload: one DeepSeek-V3 MoE layer at decode batch 1 —
 router (bf16 W_r [256,7168], fp32 bias; sigmoid, 8 groups of 32, top-4 groups,
 top-8, normalise, x2.5) + the 8 routed fp8 experts + 1 shared fp8 expert,
 weighted combine.  256 resident experts per layer, N(0,0.02) weights
@@ -12,7 +12,7 @@ rotate over `--layers` resident layer copies (11.3 GB each) and a pool of
 tokens, so no step finds its 400 MB of weights in the 256 MB MALL.
 
 Prints one JSON line.  `value` is microseconds per token at B=1 (lower is
-better); `extras` carries B=16 (config 2) and per-kernel figures.
+better); `extras` carries B=16 and per-kernel figures.
 The roofline object covers the dominant kernel (gate_up): algorithmic bytes
 per launch / its average duration measured with HIP events on the launch
 stream (cx_ctx_profile), against 8 TB/s.  cpu_baseline times the reference's
@@ -227,7 +227,7 @@ def main() -> int:
         "warmup": args.warmup, "ms_per_step": ms1, "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp8e4m3 weights x bf16 activations, fp32 accumulate",
         "data": "synthetic (counter-based generator, N(0,0.02) weights, N(0,1) tokens)",
-        "config": {"workload": "BASELINE config 1: DeepSeek-V3 MoE layer decode B=1, router + "
+        "config": {"workload": "DeepSeek-V3 MoE layer decode B=1, router + "
                                "8 routed of 256 resident fp8 experts + 1 shared, combine",
                    "tokens_per_step": 1, "resident_experts": E, "top_k": TOPK, "hidden": H,
                    "inter": I, "layers_rotated": args.layers, "token_pool": args.pool},

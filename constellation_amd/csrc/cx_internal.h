@@ -38,8 +38,30 @@ struct PlanHdr {
     int pad;
 };
 
+// Flat per-item / per-slot records written by the planner, so a workgroup
+// reaches its weight pointers with one dependent load.
+struct ItemRec {
+    const uint8_t* w_up;
+    const uint8_t* w_gate;
+    const uint8_t* w_down;
+    const float* s_up;     // scale grids; the kernel adds its row block
+    const float* s_gate;
+    const float* s_down;
+    int pb, np;            // pair range
+    int up_rb, gate_rb, down_rb, pad;
+};
+
+struct SlotRec {
+    const uint8_t* w_down;
+    const float* s_down;
+    int down_rb;
+    int pad;
+};
+
 struct PlanPtrs {
     PlanHdr* hdr;
+    ItemRec* item_rec;     // [max_items]
+    SlotRec* slot_rec;     // [max_slots]
     int* slot_expert;      // [max_slots]  index into the layer table
     int* slot_pair_begin;  // [max_slots]
     int* slot_pair_count;  // [max_slots]
@@ -49,6 +71,7 @@ struct PlanPtrs {
     int* pair_token;       // [max_pairs]
     float* pair_weight;    // [max_pairs]
     int* token_pairs;      // [T * (K+1)], pair index or -1 (shared in column K)
+    int* slot_tok_pair;    // [max_slots * 16] pair of (slot, token) or -1; T <= 16 only (nullable)
 };
 
 // Device error bits (ORed into the context's flag, read by cx_ctx_sync).
@@ -56,6 +79,7 @@ enum : int {
     kErrBadExpertId = 1,
     kErrNotResident = 2,
     kErrPlanOverflow = 4,
+    kErrDuplicateRoute = 8,
 };
 
 // ---------------------------------------------------------------------------
@@ -78,12 +102,16 @@ struct ExpertLaunch {
     float* h_f32;                 // optional [pairs, inter] fp32 h (debug/parity)
     float* y_part;                // [pairs, hidden] fp32 per-pair down output (grouped)
     void* y;                      // single mode: [T, hidden] out dtype
-    float* y_f32;                 // single mode: optional fp32 output
+    float* y_f32;                 // single mode / fused decode: optional fp32 output
     int out_dtype;
+    int fold_weight;              // phase A multiplies h by the pair's route weight
+    int np_lds;                   // >0: stage up to np_lds activation rows per item in LDS
 };
 
 hipError_t launch_gate_up(const ExpertLaunch& L, hipStream_t s);
 hipError_t launch_down(const ExpertLaunch& L, hipStream_t s);
+bool down_fused_ok(int inter);
+hipError_t launch_down_fused(const ExpertLaunch& L, int max_slots, hipStream_t s);
 hipError_t launch_combine(const PlanPtrs& plan, const float* y_part, int n_tokens,
                           int top_k, int hidden, void* y, int out_dtype, float* y_f32,
                           hipStream_t s);
@@ -97,12 +125,27 @@ hipError_t launch_generic_expert(const cx_expert_desc& e, const void* x, int in_
                                  int n_tokens, float* h_scratch, void* y, int out_dtype,
                                  float* y_f32, hipStream_t s);
 
-// Router.
-hipError_t launch_route(const void* x, int x_dtype, const void* w, int w_dtype,
-                        const float* bias, const uint8_t* resident, int n_tokens,
-                        int hidden, int n_experts, int n_group, int topk_group, int top_k,
-                        int norm, float scale, double* logits, int32_t* ids, float* wout,
-                        hipStream_t s);
+// Router (optionally followed by the planner in the same launch for T <= 16).
+struct RouteArgs {
+    const void* x;
+    int x_dtype;
+    const void* w;
+    int w_dtype;
+    const float* bias;
+    const uint8_t* resident;
+    int n_tokens, hidden, n_experts, n_group, topk_group, top_k, norm;
+    float scale;
+    double* logits;         // scratch [T, E]
+    int32_t* ids;           // [T, top_k]
+    float* wout;            // [T, top_k]
+    // planner (nullable plan = route only)
+    const PlanPtrs* plan;
+    const cx_expert_desc* table;
+    int has_shared, item_cap, max_items;
+    int* err_flag;
+};
+hipError_t launch_route(const RouteArgs& r, hipStream_t s);
+int route_max_experts();
 
 // Upload helpers / generator.
 hipError_t launch_canonicalize_fp8(uint8_t* p, uint64_t n, hipStream_t s);

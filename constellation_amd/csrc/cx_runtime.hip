@@ -194,7 +194,8 @@ int ensure(DevBuf* b, size_t bytes, hipStream_t s) {
 struct cx_ctx {
     int device = -1;
     hipStream_t own_stream = nullptr;  // for the host-buffer entry point
-    int* err_flag = nullptr;           // device int
+    int* err_flag = nullptr;           // device int: error bits of the device checks
+    int max_lds = 65536;               // dynamic LDS budget per workgroup
     DevBuf plan_buf, hhi, hlo, ypart, logits, route_ids, route_w, hscratch;
     DevBuf dx, dy;                     // cx_expert_run_host staging (device)
     void* pin_x = nullptr;             // pinned host staging
@@ -275,11 +276,17 @@ PlanSizes plan_sizes(int n_tokens, int top_k, int n_experts, int has_shared, boo
 
 int carve_plan(cx_ctx* ctx, const PlanSizes& z, int n_tokens, int top_k, hipStream_t s,
                PlanPtrs* P) {
+    const bool dense = n_tokens <= kTileTok;
+    const size_t recs = sizeof(ItemRec) * (size_t)z.max_items + sizeof(SlotRec) * (size_t)z.max_slots;
     const size_t ints = 4 + 3 * (size_t)z.max_slots + 3 * (size_t)z.max_items +
-                        2 * (size_t)z.max_pairs + (size_t)n_tokens * (top_k + 1);
-    int rc = ensure(&ctx->plan_buf, ints * 4 + 256, s);
+                        2 * (size_t)z.max_pairs + (size_t)n_tokens * (top_k + 1) +
+                        (dense ? (size_t)z.max_slots * kTileTok : 0);
+    int rc = ensure(&ctx->plan_buf, recs + ints * 4 + 256, s);
     if (rc) return rc;
-    int* base = static_cast<int*>(ctx->plan_buf.p);
+    char* raw = static_cast<char*>(ctx->plan_buf.p);
+    P->item_rec = reinterpret_cast<ItemRec*>(raw);
+    P->slot_rec = reinterpret_cast<SlotRec*>(raw + sizeof(ItemRec) * (size_t)z.max_items);
+    int* base = reinterpret_cast<int*>(raw + recs);
     P->hdr = reinterpret_cast<PlanHdr*>(base);
     int* q = base + 4;
     P->slot_expert = q; q += z.max_slots;
@@ -290,7 +297,8 @@ int carve_plan(cx_ctx* ctx, const PlanSizes& z, int n_tokens, int top_k, hipStre
     P->item_pair_count = q; q += z.max_items;
     P->pair_token = q; q += z.max_pairs;
     P->pair_weight = reinterpret_cast<float*>(q); q += z.max_pairs;
-    P->token_pairs = q;
+    P->token_pairs = q; q += (size_t)n_tokens * (top_k + 1);
+    P->slot_tok_pair = dense ? q : nullptr;
     return CX_OK;
 }
 
@@ -305,16 +313,27 @@ int check_desc(const cx_expert_desc* e) {
     return CX_OK;
 }
 
-int moe_forward(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int n_tokens,
-                const int32_t* ids, const float* w, int top_k, void* y, int out_dtype,
-                float* y_f32, hipStream_t s, bool prefill) {
+// Activation rows of one work item that fit the LDS budget next to the
+// reduction tile (<= 16 KB); 0 when staging is not worth it or not possible.
+int lds_rows(const cx_ctx* ctx, int hidden, int max_pairs_per_item) {
+    const int budget = std::min(ctx->max_lds, 65536) - 16384;
+    const int rows = budget / (hidden * 2 + 16);
+    return (max_pairs_per_item <= rows && max_pairs_per_item <= 4) ? max_pairs_per_item : 0;
+}
+
+// Routed-expert compute; when `route` is given, the router (and for T <= 16
+// the planner, in the same launch) runs first on the same stream.
+int moe_run(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int n_tokens,
+            const int32_t* ids, const float* w, int top_k, void* y, int out_dtype, float* y_f32,
+            hipStream_t s, bool prefill, RouteArgs* route) {
     if (!ctx || !layer) return fail(CX_EINVAL, "NULL context or layer");
     if (!act16(in_dtype) || !act16(out_dtype)) return fail(CX_EINVAL, "dtypes must be fp16/bf16");
     if (n_tokens <= 0 || top_k < 0 || top_k > 64) return fail(CX_EINVAL, "bad n_tokens/top_k");
     if (!x || !y || (top_k > 0 && (!ids || !w))) return fail(CX_EINVAL, "NULL buffer");
     if (!layer->fast)
         return fail(CX_EUNSUPPORTED, "layer experts do not fit the grouped kernels "
-                                     "(need hidden%%64==0, dims%%128==0, blocks 16x128 multiples)");
+                                     "(need hidden%%64==0, dims%%128==0, 128-column blocks, "
+                                     "row blocks multiple of 16)");
     int rc = set_device(ctx->device);
     if (rc) return rc;
     const PlanSizes z = plan_sizes(n_tokens, top_k, layer->n_experts, layer->has_shared, prefill);
@@ -324,8 +343,18 @@ int moe_forward(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype,
     const size_t H = layer->hidden, I = layer->inter;
     if ((rc = ensure(&ctx->hhi, (size_t)z.max_pairs * I * 2, s))) return rc;
     if ((rc = ensure(&ctx->hlo, (size_t)z.max_pairs * I * 2, s))) return rc;
-    if ((rc = ensure(&ctx->ypart, (size_t)z.max_pairs * H * 4, s))) return rc;
-    {
+    const bool fused = n_tokens <= kTileTok && down_fused_ok(layer->inter);
+    if (!fused && (rc = ensure(&ctx->ypart, (size_t)z.max_pairs * H * 4, s))) return rc;
+    if (route != nullptr) {
+        route->plan = &P;
+        route->table = layer->table;
+        route->has_shared = layer->has_shared;
+        route->item_cap = z.item_cap;
+        route->max_items = z.max_items;
+        route->err_flag = ctx->err_flag;
+        Span sp(ctx, "route", s);
+        CX_HIP(launch_route(*route, s));
+    } else {
         Span sp(ctx, "plan", s);
         CX_HIP(launch_plan(ids, w, n_tokens, top_k, layer->table, layer->n_experts,
                            layer->has_shared, z.item_cap, z.max_items, P, ctx->err_flag, s));
@@ -343,10 +372,19 @@ int moe_forward(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype,
     L.h_hi = static_cast<uint16_t*>(ctx->hhi.p);
     L.h_lo = static_cast<uint16_t*>(ctx->hlo.p);
     L.y_part = static_cast<float*>(ctx->ypart.p);
+    L.y = y;
+    L.y_f32 = y_f32;
     L.out_dtype = out_dtype;
+    L.fold_weight = fused ? 1 : 0;
+    L.np_lds = z.maxt == 1 ? lds_rows(ctx, layer->hidden, std::min(n_tokens, z.item_cap)) : 0;
     {
         Span sp(ctx, "gate_up", s);
         CX_HIP(launch_gate_up(L, s));
+    }
+    if (fused) {
+        Span sp(ctx, "down", s);
+        CX_HIP(launch_down_fused(L, z.max_slots, s));
+        return CX_OK;
     }
     {
         Span sp(ctx, "down", s);
@@ -356,6 +394,48 @@ int moe_forward(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype,
         Span sp(ctx, "combine", s);
         CX_HIP(launch_combine(P, L.y_part, n_tokens, top_k, layer->hidden, y, out_dtype, y_f32, s));
     }
+    return CX_OK;
+}
+
+int fill_route(cx_ctx* ctx, const void* x, int x_dtype, const void* w_router, int w_dtype,
+               const float* bias, const uint8_t* resident, int n_tokens, int hidden,
+               int n_experts, int n_group, int topk_group, int top_k, int norm,
+               float scale, int32_t* ids, float* wout, hipStream_t s, RouteArgs* R) {
+    if (!ctx) return fail(CX_EINVAL, "NULL context");
+    if (!x || !w_router || !bias || !ids || !wout) return fail(CX_EINVAL, "NULL buffer");
+    if ((x_dtype != CX_DTYPE_BF16 && x_dtype != CX_DTYPE_F32) ||
+        (w_dtype != CX_DTYPE_BF16 && w_dtype != CX_DTYPE_F32))
+        return fail(CX_EINVAL, "router x / weight dtype must be bf16 or fp32");
+    if (n_tokens <= 0 || hidden <= 0 || hidden % 8 != 0)
+        return fail(CX_EINVAL, "hidden must be a positive multiple of 8");
+    if (n_experts <= 0 || n_experts > 512) return fail(CX_EINVAL, "n_experts must be 1..512");
+    if (n_group <= 0 || n_group > 64 || n_experts % n_group != 0)
+        return fail(CX_EINVAL, "num_experts=%d not divisible by n_group=%d", n_experts, n_group);
+    if (topk_group <= 0 || topk_group > n_group)
+        return fail(CX_EINVAL, "invalid topk_group=%d for n_group=%d", topk_group, n_group);
+    if (top_k <= 0 || top_k > n_experts || top_k > 64)
+        return fail(CX_EINVAL, "invalid top_k=%d for num_experts=%d", top_k, n_experts);
+    int rc = set_device(ctx->device);
+    if (rc) return rc;
+    if ((rc = ensure(&ctx->logits, (size_t)n_tokens * n_experts * 8, s))) return rc;
+    *R = RouteArgs{};
+    R->x = x;
+    R->x_dtype = x_dtype;
+    R->w = w_router;
+    R->w_dtype = w_dtype;
+    R->bias = bias;
+    R->resident = resident;
+    R->n_tokens = n_tokens;
+    R->hidden = hidden;
+    R->n_experts = n_experts;
+    R->n_group = n_group;
+    R->topk_group = topk_group;
+    R->top_k = top_k;
+    R->norm = norm;
+    R->scale = scale;
+    R->logits = static_cast<double*>(ctx->logits.p);
+    R->ids = ids;
+    R->wout = wout;
     return CX_OK;
 }
 
@@ -434,8 +514,20 @@ int cx_upload_matrix(int device, const uint8_t* host_weight, uint64_t rows, uint
 }
 
 int cx_free_device(int device, void* dev_ptr) {
-    if (device < 0 || device >= 64) return fail(CX_EINVAL, "bad device");
-    return arena_free(device, dev_ptr);
+    if (device >= 64) return fail(CX_EINVAL, "bad device");
+    if (device >= 0) return arena_free(device, dev_ptr);
+    // device < 0: the caller does not track the owning device; find the arena
+    // that holds the pointer (weights of one expert never span devices).
+    if (dev_ptr == nullptr) return CX_OK;
+    for (int d = 0; d < 64; ++d) {
+        Arena& A = arena(d);
+        {
+            std::lock_guard<std::mutex> lk(A.mu);
+            if (A.live.find(dev_ptr) == A.live.end()) continue;
+        }
+        return arena_free(d, dev_ptr);
+    }
+    return fail(CX_EINVAL, "cx_free_device: %p not allocated here", dev_ptr);
 }
 
 int cx_arena_stats(int device, uint64_t* used_bytes, uint64_t* reserved_bytes) {
@@ -456,11 +548,16 @@ int cx_ctx_create(int device, cx_ctx** out) {
     if (!c) return fail(CX_ENOMEM, "out of host memory");
     c->device = device;
     if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess ||
-        hipMalloc(&c->err_flag, sizeof(int)) != hipSuccess ||
-        hipMemset(c->err_flag, 0, sizeof(int)) != hipSuccess) {
+        hipMalloc(&c->err_flag, 2 * sizeof(int)) != hipSuccess ||
+        hipMemset(c->err_flag, 0, 2 * sizeof(int)) != hipSuccess) {
         cx_ctx_destroy(c);
         return fail(CX_EHIP, "context init failed");
     }
+    int lds = 0;
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess &&
+        lds > 0)
+        c->max_lds = lds;
+    (void)hipGetLastError();
     *out = c;
     return CX_OK;
 }
@@ -554,6 +651,7 @@ int cx_expert_run(cx_ctx* ctx, const cx_expert_desc* expert, const void* x, int 
     L.y = y;
     L.y_f32 = y_f32;
     L.out_dtype = out_dtype;
+    L.np_lds = L.maxt == 1 ? lds_rows(ctx, expert->hidden, n_tokens) : 0;
     {
         Span sp(ctx, "gate_up", s);
         CX_HIP(launch_gate_up(L, s));
@@ -664,43 +762,29 @@ int cx_route(cx_ctx* ctx, const void* x, int x_dtype, const void* w_router, int 
              const float* bias, const uint8_t* resident, int n_tokens, int hidden, int n_experts,
              int n_group, int topk_group, int top_k, int norm_topk_prob,
              float routed_scaling_factor, int32_t* topk_ids, float* topk_w, void* stream) {
-    if (!ctx) return fail(CX_EINVAL, "NULL context");
-    if (!x || !w_router || !bias || !topk_ids || !topk_w) return fail(CX_EINVAL, "NULL buffer");
-    if ((x_dtype != CX_DTYPE_BF16 && x_dtype != CX_DTYPE_F32) ||
-        (w_dtype != CX_DTYPE_BF16 && w_dtype != CX_DTYPE_F32))
-        return fail(CX_EINVAL, "router x / weight dtype must be bf16 or fp32");
-    if (n_tokens <= 0 || hidden <= 0 || hidden % 8 != 0)
-        return fail(CX_EINVAL, "hidden must be a positive multiple of 8");
-    if (n_experts <= 0 || n_experts > 1024) return fail(CX_EINVAL, "n_experts must be 1..1024");
-    if (n_group <= 0 || n_group > 64 || n_experts % n_group != 0)
-        return fail(CX_EINVAL, "n_experts=%d not divisible by n_group=%d", n_experts, n_group);
-    if (topk_group <= 0 || topk_group > n_group)
-        return fail(CX_EINVAL, "invalid topk_group=%d for n_group=%d", topk_group, n_group);
-    if (top_k <= 0 || top_k > n_experts || top_k > 64)
-        return fail(CX_EINVAL, "invalid top_k=%d for num_experts=%d", top_k, n_experts);
-    int rc = set_device(ctx->device);
-    if (rc) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if ((rc = ensure(&ctx->logits, (size_t)n_tokens * n_experts * 8, s))) return rc;
+    RouteArgs R{};
+    int rc = fill_route(ctx, x, x_dtype, w_router, w_dtype, bias, resident, n_tokens, hidden,
+                        n_experts, n_group, topk_group, top_k, norm_topk_prob,
+                        routed_scaling_factor, topk_ids, topk_w, s, &R);
+    if (rc) return rc;
     Span sp(ctx, "route", s);
-    CX_HIP(launch_route(x, x_dtype, w_router, w_dtype, bias, resident, n_tokens, hidden, n_experts,
-                        n_group, topk_group, top_k, norm_topk_prob, routed_scaling_factor,
-                        static_cast<double*>(ctx->logits.p), topk_ids, topk_w, s));
+    CX_HIP(launch_route(R, s));
     return CX_OK;
 }
 
 int cx_moe_decode(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int n_tokens,
                   const int32_t* topk_ids, const float* topk_w, int top_k, void* y, int out_dtype,
                   float* y_f32, void* stream) {
-    return moe_forward(ctx, layer, x, in_dtype, n_tokens, topk_ids, topk_w, top_k, y, out_dtype,
-                       y_f32, static_cast<hipStream_t>(stream), false);
+    return moe_run(ctx, layer, x, in_dtype, n_tokens, topk_ids, topk_w, top_k, y, out_dtype,
+                   y_f32, static_cast<hipStream_t>(stream), false, nullptr);
 }
 
 int cx_moe_prefill(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int n_tokens,
                    const int32_t* topk_ids, const float* topk_w, int top_k, void* y,
                    int out_dtype, float* y_f32, void* stream) {
-    return moe_forward(ctx, layer, x, in_dtype, n_tokens, topk_ids, topk_w, top_k, y, out_dtype,
-                       y_f32, static_cast<hipStream_t>(stream), true);
+    return moe_run(ctx, layer, x, in_dtype, n_tokens, topk_ids, topk_w, top_k, y, out_dtype,
+                   y_f32, static_cast<hipStream_t>(stream), true, nullptr);
 }
 
 int cx_moe_layer(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int n_tokens,
@@ -724,12 +808,13 @@ int cx_moe_layer(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype
         if ((rc = ensure(&ctx->route_w, (size_t)n_tokens * top_k * 4, s))) return rc;
         w = static_cast<float*>(ctx->route_w.p);
     }
-    if ((rc = cx_route(ctx, x, in_dtype, w_router, w_dtype, bias, resident, n_tokens,
-                       layer->hidden, layer->n_experts, n_group, topk_group, top_k, norm_topk_prob,
-                       routed_scaling_factor, ids, w, stream)))
+    RouteArgs R{};
+    if ((rc = fill_route(ctx, x, in_dtype, w_router, w_dtype, bias, resident, n_tokens,
+                         layer->hidden, layer->n_experts, n_group, topk_group, top_k,
+                         norm_topk_prob, routed_scaling_factor, ids, w, s, &R)))
         return rc;
-    return moe_forward(ctx, layer, x, in_dtype, n_tokens, ids, w, top_k, y, out_dtype, y_f32, s,
-                       n_tokens > kTileTok);
+    return moe_run(ctx, layer, x, in_dtype, n_tokens, ids, w, top_k, y, out_dtype, y_f32, s,
+                   n_tokens > kTileTok, &R);
 }
 
 int cx_gen_fp8_matrix(cx_ctx* ctx, uint64_t seed, uint64_t stream_id, int rows, int cols,

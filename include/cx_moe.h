@@ -89,6 +89,8 @@ CX_API int cx_upload_matrix(int device,
                      uint8_t** dev_weight, float** dev_scale);
 
 /* Release one arena sub-allocation made by this library (weight or scale).
+ * device < 0 searches every device's arena for the pointer (the reference's
+ * FreeDeviceBuffer takes no device either).  NULL is a no-op.
  * Replaces FreeDeviceBuffer (backend/cuda/backend_cuda_v2.cc:55-65). */
 CX_API int cx_free_device(int device, void* dev_ptr);
 

@@ -37,8 +37,8 @@ CXO_API float cxo_fp8_decode(uint8_t v) {
 }
 
 /* fp32 -> e4m3fn, round-to-nearest-even, saturating to +-448 (0x7E/0xFE).
- * Quantiser of the synthetic experts ("quantised per
- * 128x128 block, scale = amax/448"), equal to torch.to(float8_e4m3fn) for
+ * Quantiser of the synthetic experts (quantised per 128x128 block,
+ * scale = amax/448), equal to torch.to(float8_e4m3fn) for
  * |v| <= 448.  Written on the bit pattern so CPU and GPU agree exactly. */
 CXO_API uint8_t cxo_fp8_encode(float v) {
     uint32_t bits;

@@ -114,10 +114,13 @@ def _oracle_moe(oracle, cpu, cpu_sh, x_f32, ids, wts):
     return out
 
 
-@pytest.mark.parametrize("T,prefill", [(1, False), (4, False), (16, False), (23, True), (70, True)])
-def test_moe_grouped_vs_oracle(gpu, oracle, T, prefill):
-    print(f"[moe] T={T} prefill={prefill}", flush=True)
-    E, H, I = 32, 1024, 256
+@pytest.mark.parametrize("T,prefill,I", [(1, False, 512), (3, False, 512), (4, False, 512),
+                                         (16, False, 512), (23, True, 512), (70, True, 512),
+                                         (2, False, 256), (40, True, 256)])
+def test_moe_grouped_vs_oracle(gpu, oracle, T, prefill, I):
+    """T <= 16: fused decode down + combine (I=512) or per-pair + combine (I=256)."""
+    print(f"[moe] T={T} prefill={prefill} I={I}", flush=True)
+    E, H = 32, 1024
     layer, experts, sh, cpu, cpu_sh = _make_layer(gpu, oracle, E, H, I, seed=11)
     try:
         x, w, bias = _router_inputs(gpu, 12, T, E, H, bias_skew=0.3 if T > 16 else 0.0)
@@ -137,7 +140,7 @@ def test_moe_grouped_vs_oracle(gpu, oracle, T, prefill):
 def test_moe_prefill_hot_expert_splits_items(gpu, oracle):
     """One expert routed by every token (> 64 pairs -> several work items)."""
     print("[moe] hot expert", flush=True)
-    E, H, I, T = 16, 1024, 256, 150
+    E, H, I, T = 16, 1024, 512, 150
     layer, experts, sh, cpu, cpu_sh = _make_layer(gpu, oracle, E, H, I, seed=21, shared=False)
     try:
         x = gpu.gen_normal(22, 1, (T, H), 1.0, torch.float16)
@@ -156,7 +159,7 @@ def test_moe_prefill_hot_expert_splits_items(gpu, oracle):
 
 def test_moe_layer_fused_router(gpu, oracle):
     print("[moe] fused layer", flush=True)
-    E, H, I, T = 32, 1024, 256, 3
+    E, H, I, T = 32, 1024, 512, 3
     layer, experts, sh, cpu, cpu_sh = _make_layer(gpu, oracle, E, H, I, seed=31)
     try:
         x, w, bias = _router_inputs(gpu, 32, T, E, H)
@@ -176,7 +179,7 @@ def test_moe_bad_and_missing_experts_reported(gpu):
     print("[moe] error flags", flush=True)
     from constellation_amd import CxError
     from constellation_amd.engine import Expert, Layer
-    H, I = 1024, 256
+    H, I = 1024, 512
     e0 = Expert.generate(0, 1, 0x10, hidden=H, inter=I)
     layer = Layer(gpu, [e0, None, None, None])
     try:
@@ -215,5 +218,30 @@ def test_full_size_decode_layer(gpu, oracle, T):
                           x.float().cpu().numpy(), idn, wn)
         yf = yf.cpu().numpy()
         assert rel_l2(yf, ref) < 1e-5 and np.abs(yf - ref).max() < 2e-2
+    finally:
+        _free(layer, experts, sh)
+
+
+@pytest.mark.parametrize("T,prefill", [(2, False), (20, True)])
+def test_moe_duplicate_route_is_dropped_and_reported(gpu, oracle, T, prefill):
+    """validate_routes (server/moe_layer_runtime.py:84-98) rejects a token that
+    lists the same expert twice; the engine drops the repeat and reports it."""
+    print(f"[moe] duplicate routes T={T}", flush=True)
+    from constellation_amd import CxError
+    E, H, I = 8, 1024, 512
+    layer, experts, sh, cpu, cpu_sh = _make_layer(gpu, oracle, E, H, I, seed=51, shared=False)
+    try:
+        x = gpu.gen_normal(52, 1, (T, H), 1.0, torch.bfloat16)
+        ids = np.tile(np.array([[1, 3]], np.int32), (T, 1))
+        ids[0] = [2, 2]
+        wts = np.full(ids.shape, 0.5, np.float32)
+        y, yf = gpu.moe(layer, x, torch.from_numpy(ids).cuda(), torch.from_numpy(wts).cuda(),
+                        want_f32=True, prefill=prefill)
+        with pytest.raises(CxError):
+            gpu.sync()
+        kept = ids.copy()
+        kept[0] = [2, -1]
+        ref = _oracle_moe(oracle, cpu, None, x.float().cpu().numpy(), kept, wts)
+        assert rel_l2(yf.cpu().numpy(), ref) < 1e-5
     finally:
         _free(layer, experts, sh)
