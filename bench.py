@@ -50,7 +50,40 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-b16", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
+    ap.add_argument("--no-extra-configs", action="store_true",
+                    help="skip the single-expert, prefill and node-share measurements")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="first run a plain device copy of this many MiB (three times): the "
+                         "known-size kernel that scales HBM counters of a --pmc profile")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = "profiles/k_gate_up_decode_b1_pmc.txt"
+
+
+def measured_traffic():
+    """HBM bytes per k_gate_up launch at B=1 from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor), or None."""
+    import re
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_FILE)
+    try:
+        with open(path) as f:
+            m = re.search(r"^traffic_bytes_per_launch\s*=\s*([0-9.eE+]+)", f.read(), re.M)
+    except OSError:
+        return None
+    return float(m.group(1)) if m else None
+
+
+def copy_calibration(mib: int) -> None:
+    import torch
+    n = mib << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"copy calibration: 3 x {n} bytes read + {n} bytes written", file=sys.stderr)
 
 
 def build_layers(ctx, n_layers):
@@ -129,6 +162,157 @@ def gate_up_bytes(T, U):
     return (U + 1) * (2 * I * H + 2 * SCALE_BYTES) + T * H * 2
 
 
+def zipf_bias(bias, alpha: float, seed: int):
+    """Config-3/4 skew: bias_e += alpha * rank(e)^-1.1, ranks from a seeded
+    permutation of the experts (alpha 0.25 gives per-expert counts from 0 to
+    ~150 at T=512)."""
+    import numpy as np
+    import torch
+    perm = np.random.default_rng(seed).permutation(E)
+    rank = np.empty(E)
+    rank[perm] = np.arange(1, E + 1)
+    return bias + torch.from_numpy((alpha * rank ** -1.1).astype(np.float32)).to(bias.device)
+
+
+def bench_single_expert(ctx, layers, steps):
+    """Config 0: one routed expert, one token, device-resident in/out (rotating
+    over 64 experts so no call finds its weights in the MALL), plus the
+    host-buffer entry point (pinned H2D + kernels + D2H, as RunExpertRequest)."""
+    import torch
+    from constellation_amd import FP16
+    experts = layers[0]["experts"][:64]
+    x = ctx.gen_normal(SEED, 0x900, (1, H), 1.0, torch.bfloat16)
+    for i in range(16):
+        ctx.expert_run(experts[i % 64], x)
+    torch.cuda.synchronize()
+    ctx.profile(True)
+    for i in range(steps):
+        ctx.expert_run(experts[i % 64], x)
+    torch.cuda.synchronize()
+    gu, dn = ctx.profile_read("gate_up"), ctx.profile_read("down")
+    ctx.profile(False)
+    dev_us = (gu[1] + dn[1]) * 1e3 / gu[0]
+    alg = EXPERT_BYTES + 2 * H * 2
+    xh = x.cpu().to(torch.float16).view(torch.int16).numpy().tobytes()
+    for i in range(8):
+        ctx.expert_run_host(experts[i % 64], xh, FP16, 1, FP16)
+    t0 = time.perf_counter()
+    n = max(50, steps // 4)
+    for i in range(n):
+        ctx.expert_run_host(experts[i % 64], xh, FP16, 1, FP16)
+    host_us = (time.perf_counter() - t0) / n * 1e6
+    return {"device_us_per_expert": dev_us, "gate_up_us": gu[1] * 1e3 / gu[0],
+            "down_us": dn[1] * 1e3 / dn[0], "algorithmic_bytes": alg,
+            "gbs": alg / (dev_us * 1e-6) / 1e9,
+            "host_buffer_us_per_request": host_us,
+            "host_buffer_note": "cx_expert_run_host, fp16 in/out, wall clock incl. pinned "
+                                "H2D/D2H and stream sync (PCIe-inclusive)"}
+
+
+def bench_prefill(ctx, layers, steps):
+    """Config 3: a 512-token prefill chunk through router + grouped GEMM, with
+    the Zipf-skewed correction bias (alpha 0.25)."""
+    import torch
+    T = 512
+    x = ctx.gen_normal(SEED, 0x7000, (T, H), 1.0, torch.bfloat16)
+    outs = (torch.empty((T, H), dtype=torch.bfloat16, device=x.device), None,
+            torch.empty((T, TOPK), dtype=torch.int32, device=x.device),
+            torch.empty((T, TOPK), dtype=torch.float32, device=x.device))
+    biases = [zipf_bias(l["bias"], 0.25, SEED) for l in layers]
+
+    def step(i):
+        l = layers[i % len(layers)]
+        ctx.moe_layer(l["layer"], x, l["w_r"], biases[i % len(layers)], n_group=NGROUP,
+                      topk_group=TOPK_GROUP, top_k=TOPK, norm_topk_prob=True,
+                      routed_scaling_factor=SCALE, out=outs)
+    for i in range(3):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(steps):
+        step(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    ctx.sync()
+    ms = ev0.elapsed_time(ev1) / steps
+    ids = outs[2].cpu()
+    counts = torch.bincount(ids.flatten().long(), minlength=E)
+    U = int((counts > 0).sum())
+    ctx.profile(True)
+    for i in range(4):
+        step(i)
+    torch.cuda.synchronize()
+    kern = {k: ctx.profile_read(k) for k in ("route", "plan", "gate_up", "down", "combine")}
+    ctx.profile(False)
+    flops = (T * TOPK + T) * 6.0 * I * H + 2.0 * T * E * H
+    alg = (U + 1) * EXPERT_BYTES + ROUTER_BYTES + 2 * T * H * 2
+    attainable = min(5.0e15, flops / alg * HBM_PEAK_GBS * 1e9)
+    return {"tokens": T, "us_per_chunk": ms * 1e3, "distinct_routed_experts": U,
+            "max_tokens_per_expert": int(counts.max()), "flop": flops, "algorithmic_bytes": alg,
+            "tflops": flops / (ms * 1e-3) / 1e12, "gbs": alg / (ms * 1e-3) / 1e9,
+            "attainable_tflops_at_8tbs": attainable / 1e12,
+            "frac_of_attainable": flops / (ms * 1e-3) / attainable,
+            "frac_of_fp8_peak": flops / (ms * 1e-3) / 5.0e15,
+            "kernels": {k: {"launches": n, "avg_us": (t * 1e3 / n) if n else None}
+                        for k, (n, t) in kern.items()}}
+
+
+def bench_node_share(ctx, sweeps):
+    """Config 4: one expert node's resident share, 58 layers x 64 experts
+    (e = 0 mod 4, no shared expert; ~163.5 GB), batch 32 per layer with routes
+    precomputed by the HIP router under the Zipf bias restricted to the
+    resident set; times sweeps over all 58 layers."""
+    import torch
+    from constellation_amd.engine import Expert, Layer
+    n_layers, T = 58, 32
+    resident = list(range(0, E, 4))
+    mask = torch.zeros(E, dtype=torch.uint8, device="cuda")
+    mask[resident] = 1
+    layers, all_experts, routes = [], [], []
+    x = ctx.gen_normal(SEED, 0x7100, (T, H), 1.0, torch.bfloat16)
+    for l in range(n_layers):
+        ex = [None] * E
+        for e in resident:
+            ex[e] = Expert.generate(0, SEED + 1, stream_base(l, e))
+            all_experts.append(ex[e])
+        layers.append(Layer(ctx, ex, None))
+        w_r = ctx.gen_normal(SEED + 1, stream_base(l, 1000) + 1, (E, H), 0.02, torch.bfloat16)
+        bias = zipf_bias(ctx.gen_normal(SEED + 1, stream_base(l, 1000) + 2, (E,), 0.01,
+                                        torch.float32), 0.25, SEED + l)
+        routes.append(ctx.route(x, w_r, bias, resident=mask, n_group=NGROUP,
+                                topk_group=TOPK_GROUP, top_k=TOPK, norm_topk_prob=True,
+                                routed_scaling_factor=SCALE))
+    torch.cuda.synchronize()
+    uniq = [len(set(r[0].flatten().tolist()) - {-1}) for r in routes]
+    y = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+
+    def sweep():
+        for l in range(n_layers):
+            ids, w = routes[l]
+            ctx.moe(layers[l], x, ids, w, out_dtype=torch.bfloat16)
+    sweep()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(sweeps):
+        sweep()
+    ev1.record()
+    torch.cuda.synchronize()
+    ctx.sync()
+    ms = ev0.elapsed_time(ev1) / sweeps
+    alg = sum(u * EXPERT_BYTES + 2 * T * H * 2 for u in uniq)
+    out = {"layers": n_layers, "resident_per_layer": len(resident), "tokens_per_layer": T,
+           "resident_bytes": len(all_experts) * EXPERT_BYTES, "ms_per_sweep": ms,
+           "us_per_layer": ms * 1e3 / n_layers, "mean_distinct_experts": sum(uniq) / len(uniq),
+           "gbs": alg / (ms * 1e-3) / 1e9, "frac_of_8tbs": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    for lay in layers:
+        lay.close()
+    for e in all_experts:
+        e.free()
+    return out
+
+
 def cpu_baseline(budget_s: float):
     """Reference CPU expert path on host cores: per token, the fp64 router
     (this repo's port) + 9 sequential expert runs through the reference's own
@@ -164,7 +348,7 @@ def cpu_baseline(budget_s: float):
             run(runners[(tokens * TOPK + j) % n_pool], x)
         run(runners[-1], x)
         tokens += 1
-        if time.perf_counter() - t0 > budget_s or tokens >= 200:
+        if time.perf_counter() - t0 > budget_s:
             break
     dt = time.perf_counter() - t0
     for r in runners:
@@ -187,6 +371,8 @@ def main() -> int:
     from constellation_amd.engine import Context, device_info
 
     info = device_info(0)
+    if args.copy_calibration_mb > 0:
+        copy_calibration(args.copy_calibration_mb)
     ctx = Context(0)
     t_gen = time.perf_counter()
     layers = build_layers(ctx, args.layers)
@@ -211,13 +397,24 @@ def main() -> int:
                          "layer_gbs": layer_bytes(16, u16) / (ms16 * 1e-3) / 1e9,
                          "layer_frac_of_8tbs": layer_bytes(16, u16) / (ms16 * 1e-3) / 1e9 / HBM_PEAK_GBS,
                          "kernels": prof16}
+    if not args.no_extra_configs:
+        extras["config0_single_expert"] = bench_single_expert(ctx, layers, max(100, args.steps // 2))
+        extras["config3_prefill"] = bench_prefill(ctx, layers, 10)
+    for L in layers:  # release the rotated layers before the node-share residency
+        L["layer"].close()
+        for e in L["experts"] + [L["shared"]]:
+            e.free()
+    layers = None
+    if not args.no_extra_configs:
+        extras["config4_node_share"] = bench_node_share(ctx, 5)
     gu = prof1["gate_up"]
     gu_bytes = gate_up_bytes(1, u1)
     gu_gbs = gu_bytes / (gu["avg_us"] * 1e-6) / 1e9 if gu["avg_us"] else None
     roofline = {"bound": "hbm", "kernel": "k_gate_up (B=1 decode)", "achieved": gu_gbs,
                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": (gu_gbs / HBM_PEAK_GBS) if gu_gbs else None,
-                "algorithmic_bytes_per_launch": gu_bytes, "traffic": None}
+                "algorithmic_bytes_per_launch": gu_bytes, "traffic": measured_traffic(),
+                "traffic_source": TRAFFIC_FILE}
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(args.cpu_seconds)
@@ -236,11 +433,6 @@ def main() -> int:
         "extras": extras,
     }
     print(json.dumps(line), flush=True)
-    for L in layers:
-        L["layer"].close()
-        for e in L["experts"]:
-            e.free()
-        L["shared"].free()
     ctx.close()
     return 0
 

@@ -6,8 +6,11 @@ include/cx_moe.h (libcx_moe.so).
 Python modules:
   _lib               ctypes binding of the C ABI (no fallback)
   engine             torch-tensor handles: Context, Expert, Layer
-  moe_layer_runtime  mirror of server/moe_layer_runtime.py's router/combine API
-  expert_backend     mirror of the expert_node_v2 backend plugin contract
+  moe_layer_runtime  route_token_real / route_tokens: the server's router API
+                     (server/moe_layer_runtime.py:232-408) on the HIP router
+
+C++ (backend_amd/): the expert_node_v2 AMD backend plugin (upload/free,
+GPU info, BackendWorkspaceAmdV2) over the same C ABI.
   build              hipcc build of libcx_moe.so
 """
 from ._lib import BF16, F32, FP16, CxError, EXPORTED, LIB_PATH  # noqa: F401

@@ -1025,9 +1025,9 @@ void go_gate_up(const ExpertLaunch& L, dim3 grid, hipStream_t s) {
     constexpr int D = NKB < 4 ? NKB : 4;
     if (MAXT == 1 && L.np_lds > 0) {
         const size_t lds = (size_t)L.np_lds * ((size_t)L.hidden * 2 + 16);
-        hipLaunchKernelGGL((k_gate_up_t<NKB, D, MAXT, F16, true, KS>), grid, dim3(64 * KS), lds, s, L);
+        cx_launch((k_gate_up_t<NKB, D, MAXT, F16, true, KS>), grid, dim3(64 * KS), lds, s, L);
     } else {
-        hipLaunchKernelGGL((k_gate_up_t<NKB, D, MAXT, F16, false, KS>), grid, dim3(64 * KS), 0, s, L);
+        cx_launch((k_gate_up_t<NKB, D, MAXT, F16, false, KS>), grid, dim3(64 * KS), 0, s, L);
     }
 }
 
@@ -1056,8 +1056,8 @@ bool pick_gate_up(const ExpertLaunch& L, dim3 grid, hipStream_t s) {
 template <int MAXT>
 bool pick_down(const ExpertLaunch& L, dim3 grid, hipStream_t s) {
     switch (L.inter / kKB) {
-        case 4: hipLaunchKernelGGL((k_down_t<4, 4, MAXT>), grid, dim3(256), 0, s, L); return true;
-        case 16: hipLaunchKernelGGL((k_down_t<16, 4, MAXT>), grid, dim3(256), 0, s, L); return true;
+        case 4: cx_launch((k_down_t<4, 4, MAXT>), grid, dim3(256), 0, s, L); return true;
+        case 16: cx_launch((k_down_t<16, 4, MAXT>), grid, dim3(256), 0, s, L); return true;
         default: return false;
     }
 }
@@ -1074,11 +1074,11 @@ hipError_t launch_gate_up(const ExpertLaunch& L, hipStream_t s) {
     else done = f16 ? pick_gate_up<4, true>(L, grid, s) : pick_gate_up<4, false>(L, grid, s);
     if (!done) {
         if (L.maxt == 1) {
-            if (f16) hipLaunchKernelGGL((k_gate_up_rt<1, true>), grid, dim3(256), 0, s, L);
-            else hipLaunchKernelGGL((k_gate_up_rt<1, false>), grid, dim3(256), 0, s, L);
+            if (f16) cx_launch((k_gate_up_rt<1, true>), grid, dim3(256), 0, s, L);
+            else cx_launch((k_gate_up_rt<1, false>), grid, dim3(256), 0, s, L);
         } else {
-            if (f16) hipLaunchKernelGGL((k_gate_up_rt<4, true>), grid, dim3(256), 0, s, L);
-            else hipLaunchKernelGGL((k_gate_up_rt<4, false>), grid, dim3(256), 0, s, L);
+            if (f16) cx_launch((k_gate_up_rt<4, true>), grid, dim3(256), 0, s, L);
+            else cx_launch((k_gate_up_rt<4, false>), grid, dim3(256), 0, s, L);
         }
     }
     return hipGetLastError();
@@ -1090,8 +1090,8 @@ hipError_t launch_down(const ExpertLaunch& L, hipStream_t s) {
     const dim3 grid(L.hidden / (kTileRows * kWaves), items);
     const bool done = L.maxt == 1 ? pick_down<1>(L, grid, s) : pick_down<4>(L, grid, s);
     if (!done) {
-        if (L.maxt == 1) hipLaunchKernelGGL((k_down_rt<1>), grid, dim3(256), 0, s, L);
-        else hipLaunchKernelGGL((k_down_rt<4>), grid, dim3(256), 0, s, L);
+        if (L.maxt == 1) cx_launch((k_down_rt<1>), grid, dim3(256), 0, s, L);
+        else cx_launch((k_down_rt<4>), grid, dim3(256), 0, s, L);
     }
     return hipGetLastError();
 }
@@ -1106,7 +1106,7 @@ int down_fused_rg() {
 
 template <int NKBW, int KS, int RG>
 void go_down_fused(const ExpertLaunch& L, size_t lds, hipStream_t s) {
-    hipLaunchKernelGGL((k_down_fused<NKBW, KS, RG>), dim3(L.hidden / (kTileRows * RG)), dim3(64 * KS),
+    cx_launch((k_down_fused<NKBW, KS, RG>), dim3(L.hidden / (kTileRows * RG)), dim3(64 * KS),
                        lds, s, L);
 }
 
@@ -1142,7 +1142,7 @@ hipError_t launch_down_fused(const ExpertLaunch& L, int max_slots, hipStream_t s
 hipError_t launch_combine(const PlanPtrs& plan, const float* y_part, int n_tokens, int top_k,
                           int hidden, void* y, int out_dtype, float* y_f32, hipStream_t s) {
     const int n = n_tokens * (hidden / 4);
-    hipLaunchKernelGGL(k_combine, dim3((n + 255) / 256), dim3(256), 0, s, plan, y_part,
+    cx_launch(k_combine, dim3((n + 255) / 256), dim3(256), 0, s, plan, y_part,
                        n_tokens, top_k, hidden, y, out_dtype, y_f32);
     return hipGetLastError();
 }
@@ -1151,11 +1151,11 @@ hipError_t launch_generic_expert(const cx_expert_desc& e, const void* x, int in_
                                  int n_tokens, float* h_scratch, void* y, int out_dtype,
                                  float* y_f32, hipStream_t s) {
     const int n1 = n_tokens * e.inter, n2 = n_tokens * e.hidden;
-    hipLaunchKernelGGL(k_generic_gate_up, dim3((n1 + 127) / 128), dim3(128), 0, s, e, x,
+    cx_launch(k_generic_gate_up, dim3((n1 + 127) / 128), dim3(128), 0, s, e, x,
                        in_dtype, n_tokens, h_scratch);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_generic_down, dim3((n2 + 127) / 128), dim3(128), 0, s, e, h_scratch,
+    cx_launch(k_generic_down, dim3((n2 + 127) / 128), dim3(128), 0, s, e, h_scratch,
                        n_tokens, y, out_dtype, y_f32);
     return hipGetLastError();
 }

@@ -191,7 +191,7 @@ hipError_t launch_gen_normal(uint64_t seed, uint64_t stream_id, uint64_t count, 
     uint64_t blocks = (count + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_gen_normal, dim3((unsigned)blocks), dim3(256), 0, s, base, count, std_dev,
+    cx_launch(k_gen_normal, dim3((unsigned)blocks), dim3(256), 0, s, base, count, std_dev,
                        dtype, out);
     return hipGetLastError();
 }
@@ -200,7 +200,7 @@ hipError_t launch_gen_fp8(uint64_t seed, uint64_t stream_id, int rows, int cols,
                           float std_dev, uint8_t* q, float* scale, hipStream_t s) {
     const uint64_t base = mix64_host(seed, stream_id);
     const int nblk = ((rows + rb - 1) / rb) * ((cols + cb - 1) / cb);
-    hipLaunchKernelGGL(k_gen_fp8, dim3(nblk), dim3(256), 0, s, base, rows, cols, rb, cb, std_dev,
+    cx_launch(k_gen_fp8, dim3(nblk), dim3(256), 0, s, base, rows, cols, rb, cb, std_dev,
                        q, scale);
     return hipGetLastError();
 }
@@ -209,7 +209,7 @@ hipError_t launch_canonicalize_fp8(uint8_t* p, uint64_t n, hipStream_t s) {
     uint64_t blocks = (n + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_canonicalize, dim3((unsigned)blocks), dim3(256), 0, s, p, n);
+    cx_launch(k_canonicalize, dim3((unsigned)blocks), dim3(256), 0, s, p, n);
     return hipGetLastError();
 }
 

@@ -2,6 +2,7 @@
 // the public ABI; include/cx_moe.h is).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -81,6 +82,29 @@ enum : int {
     kErrPlanOverflow = 4,
     kErrDuplicateRoute = 8,
 };
+
+// ---------------------------------------------------------------------------
+// Kernel-duration timing.  While a LaunchTimer is current on the calling
+// thread, cx_launch passes its events to hipExtLaunchKernelGGL, so the start
+// event takes the first kernel's start timestamp and the stop event the last
+// kernel's end timestamp (dispatch timestamps, without launch gaps).
+struct LaunchTimer {
+    hipEvent_t start = nullptr, stop = nullptr;
+    bool started = false;
+};
+LaunchTimer*& current_launch_timer();
+
+template <typename F, typename... Args>
+inline void cx_launch(F kernel, dim3 grid, dim3 block, uint32_t lds, hipStream_t s, Args... args) {
+    LaunchTimer* t = current_launch_timer();
+    if (t == nullptr) {
+        kernel<<<grid, block, lds, s>>>(args...);
+        return;
+    }
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, s, t->started ? nullptr : t->start, t->stop, 0u,
+                          args...);
+    t->started = true;
+}
 
 // ---------------------------------------------------------------------------
 // Launchers (defined in the .hip files).  All return hipError_t of the launch.

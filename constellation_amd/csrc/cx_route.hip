@@ -821,10 +821,10 @@ hipError_t launch_route(const RouteArgs& R, hipStream_t s) {
     const size_t sel = A.epl ? 0 : select_lds(R.n_experts);
     const dim3 lg(R.n_experts, (R.n_tokens + kRouteTB - 1) / kRouteTB);
     const bool xf = R.x_dtype == CX_DTYPE_F32, wf = R.w_dtype == CX_DTYPE_F32;
-    if (xf && wf) hipLaunchKernelGGL((k_route_logits<true, true>), lg, dim3(kRouteThreads), 0, s, A);
-    else if (xf) hipLaunchKernelGGL((k_route_logits<true, false>), lg, dim3(kRouteThreads), 0, s, A);
-    else if (wf) hipLaunchKernelGGL((k_route_logits<false, true>), lg, dim3(kRouteThreads), 0, s, A);
-    else hipLaunchKernelGGL((k_route_logits<false, false>), lg, dim3(kRouteThreads), 0, s, A);
+    if (xf && wf) cx_launch((k_route_logits<true, true>), lg, dim3(kRouteThreads), 0, s, A);
+    else if (xf) cx_launch((k_route_logits<true, false>), lg, dim3(kRouteThreads), 0, s, A);
+    else if (wf) cx_launch((k_route_logits<false, true>), lg, dim3(kRouteThreads), 0, s, A);
+    else cx_launch((k_route_logits<false, false>), lg, dim3(kRouteThreads), 0, s, A);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     if (R.n_tokens <= kRouteTB) {
@@ -833,10 +833,10 @@ hipError_t launch_route(const RouteArgs& R, hipStream_t s) {
         size_t lds = A.epl ? 0 : (size_t)2 * (threads / 64) * R.n_experts * sizeof(double) + (threads / 64) * 64;
         const size_t plan_lds = plan_wave_lds(R.n_experts, R.n_tokens, R.top_k);
         if (A.do_plan && plan_lds > lds) lds = plan_lds;
-        hipLaunchKernelGGL(k_route_select_plan, dim3(1), dim3(threads), lds, s, A);
+        cx_launch(k_route_select_plan, dim3(1), dim3(threads), lds, s, A);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(k_route_select, dim3((R.n_tokens + 3) / 4), dim3(kRouteThreads), sel, s, A);
+    cx_launch(k_route_select, dim3((R.n_tokens + 3) / 4), dim3(kRouteThreads), sel, s, A);
     err = hipGetLastError();
     if (err != hipSuccess || R.plan == nullptr) return err;
     return launch_plan(R.ids, R.wout, R.n_tokens, R.top_k, R.table, R.n_experts, R.has_shared,
@@ -847,13 +847,13 @@ hipError_t launch_plan(const int32_t* ids, const float* w, int n_tokens, int top
                        const cx_expert_desc* table, int n_experts, int has_shared, int item_cap,
                        int max_items, PlanPtrs plan, int* err_flag, hipStream_t s) {
     if (n_tokens <= kTileTok && item_cap >= kTileTok && plan.slot_tok_pair != nullptr) {
-        hipLaunchKernelGGL(k_plan_wave, dim3(1), dim3(64), plan_wave_lds(n_experts, n_tokens, top_k),
+        cx_launch(k_plan_wave, dim3(1), dim3(64), plan_wave_lds(n_experts, n_tokens, top_k),
                            s, ids, w, n_tokens, top_k, table, n_experts, has_shared, plan, err_flag);
         return hipGetLastError();
     }
     const int threads = n_tokens * top_k <= 512 ? 256 : kPlanThreads;
     const size_t lds = sizeof(int) * (2 * (size_t)n_experts + threads);
-    hipLaunchKernelGGL(k_plan, dim3(1), dim3(threads), lds, s, ids, w, n_tokens, top_k, table,
+    cx_launch(k_plan, dim3(1), dim3(threads), lds, s, ids, w, n_tokens, top_k, table,
                        n_experts, has_shared, item_cap, max_items, plan, err_flag);
     return hipGetLastError();
 }

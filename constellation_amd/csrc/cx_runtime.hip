@@ -207,6 +207,13 @@ struct cx_ctx {
     std::map<std::string, std::pair<int, double>> totals;
 };
 
+namespace cx {
+LaunchTimer*& current_launch_timer() {
+    static thread_local LaunchTimer* t = nullptr;
+    return t;
+}
+}  // namespace cx
+
 struct cx_layer {
     int n_experts = 0;
     int has_shared = 0;
@@ -217,29 +224,41 @@ struct cx_layer {
 
 namespace {
 
-// Records start/end events around one kernel launch when profiling is on.
+// Times the kernels launched in its scope when profiling is on: the launches
+// carry the events (cx_launch), so the span is first-kernel start to
+// last-kernel end as the command processor stamps them.
 class Span {
 public:
-    Span(cx_ctx* ctx, const char* name, hipStream_t s) : ctx_(ctx), s_(s) {
+    Span(cx_ctx* ctx, const char* name, hipStream_t s) : ctx_(ctx) {
+        (void)s;
         if (!ctx_->prof) return;
-        if (hipEventCreate(&a_) != hipSuccess || hipEventCreate(&b_) != hipSuccess) {
+        if (hipEventCreate(&t_.start) != hipSuccess || hipEventCreate(&t_.stop) != hipSuccess) {
             (void)hipGetLastError();
-            a_ = b_ = nullptr;
+            if (t_.start) (void)hipEventDestroy(t_.start);
+            t_.start = t_.stop = nullptr;
             return;
         }
-        (void)hipEventRecord(a_, s_);
         name_ = name;
+        prev_ = current_launch_timer();
+        current_launch_timer() = &t_;
+        active_ = true;
     }
     ~Span() {
-        if (a_ == nullptr) return;
-        (void)hipEventRecord(b_, s_);
-        ctx_->spans[name_].push_back({a_, b_});
+        if (!active_) return;
+        current_launch_timer() = prev_;
+        if (t_.started) {
+            ctx_->spans[name_].push_back({t_.start, t_.stop});
+        } else {
+            (void)hipEventDestroy(t_.start);
+            (void)hipEventDestroy(t_.stop);
+        }
     }
 
 private:
     cx_ctx* ctx_;
-    hipStream_t s_;
-    hipEvent_t a_ = nullptr, b_ = nullptr;
+    LaunchTimer t_;
+    LaunchTimer* prev_ = nullptr;
+    bool active_ = false;
     std::string name_;
 };
 
