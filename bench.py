@@ -158,8 +158,9 @@ def layer_bytes(T, U):
 
 
 def gate_up_bytes(T, U):
-    # gate + up weights and scales of every active expert (U routed + shared) + x in
-    return (U + 1) * (2 * I * H + 2 * SCALE_BYTES) + T * H * 2
+    # the routed gate/up launch: gate + up weights and scales of the U routed
+    # experts + x in (the shared expert's gate/up runs beside the router)
+    return U * (2 * I * H + 2 * SCALE_BYTES) + T * H * 2
 
 
 def zipf_bias(bias, alpha: float, seed: int):

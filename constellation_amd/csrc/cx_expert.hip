@@ -29,124 +29,11 @@
 //    is valid; loads stay contiguous.
 #include <cstdlib>
 
-#include "cx_internal.h"
+#include "cx_down.h"
+#include "cx_gate_up.h"
 
 namespace cx {
 namespace {
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ bf16x8 cvt8_bf16(uint32_t w0, uint32_t w1) {
-    const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false);
-    const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true);
-    const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
-    const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
-    return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-}
-
-__device__ __forceinline__ f16x8 cvt8_f16(uint32_t w0, uint32_t w1) {
-    const f16x2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false);
-    const f16x2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true);
-    const f16x2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false);
-    const f16x2 d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true);
-    return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-}
-
-template <bool F16>
-struct Mma;
-
-template <>
-struct Mma<false> {
-    typedef bf16x8 V;
-    static __device__ __forceinline__ V cvt(uint32_t a, uint32_t b) { return cvt8_bf16(a, b); }
-    static __device__ __forceinline__ V bits(u32x4 v) { return __builtin_bit_cast(V, v); }
-    static __device__ __forceinline__ f32x4 mma(V a, V b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-    }
-};
-
-template <>
-struct Mma<true> {
-    typedef f16x8 V;
-    static __device__ __forceinline__ V cvt(uint32_t a, uint32_t b) { return cvt8_f16(a, b); }
-    static __device__ __forceinline__ V bits(u32x4 v) { return __builtin_bit_cast(V, v); }
-    static __device__ __forceinline__ f32x4 mma(V a, V b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-    }
-};
-
-// 16-byte load from global memory.  The explicit global address space keeps
-// the compiler from emitting FLAT loads (which also count against lgkmcnt,
-// so any LDS access would drain the whole weight-prefetch ring).
-typedef __attribute__((address_space(1))) const u32x4 global_u32x4;
-__device__ __forceinline__ u32x4 ld16(const void* p) {
-    return *(global_u32x4*)(p);
-}
-
-__device__ __forceinline__ float ldf(const float* p) {
-    return *(__attribute__((address_space(1))) const float*)(p);
-}
-
-__device__ __forceinline__ int ldi(const int* p) {
-    return *(__attribute__((address_space(1))) const int*)(p);
-}
-
-// fp32 -> bf16 bits, round to nearest even (finite inputs; NaN kept quiet).
-__device__ __forceinline__ uint32_t bf16_rne(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return u >> 16;
-}
-
-__device__ __forceinline__ uint32_t f16_rne(float f) {
-    const _Float16 h = static_cast<_Float16>(f);  // v_cvt_f16_f32: RNE
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h));
-}
-
-__device__ __forceinline__ uint32_t cast_out(float f, int out_dtype) {
-    return out_dtype == CX_DTYPE_FP16 ? f16_rne(f) : bf16_rne(f);
-}
-
-// Resolves the work unit of this workgroup.  Returns false if the
-// workgroup has no work (grid is sized for the worst case).
-struct Unit {
-    cx_expert_desc e;
-    int pb;  // first pair
-    int np;  // pairs in this unit
-};
-
-__device__ __forceinline__ bool resolve_unit(const ExpertLaunch& L, int unit_cap, Unit* u) {
-    const int item = blockIdx.y;
-    if (L.table != nullptr) {
-        if (item >= L.plan.hdr->n_items) return false;
-        const ItemRec r = L.plan.item_rec[item];
-        u->pb = r.pb;
-        u->np = r.np;
-        u->e.w_up = r.w_up;
-        u->e.w_gate = r.w_gate;
-        u->e.w_down = r.w_down;
-        u->e.s_up = r.s_up;
-        u->e.s_gate = r.s_gate;
-        u->e.s_down = r.s_down;
-        u->e.hidden = L.hidden;
-        u->e.inter = L.inter;
-        u->e.up_rb = r.up_rb;
-        u->e.gate_rb = r.gate_rb;
-        u->e.down_rb = r.down_rb;
-        u->e.up_cb = u->e.gate_cb = u->e.down_cb = kKB;  // grouped layers are 128-column blocks
-    } else {
-        u->pb = item * unit_cap;
-        if (u->pb >= L.n_tokens) return false;
-        u->np = min(unit_cap, L.n_tokens - u->pb);
-        u->e = L.single;
-    }
-    return u->np > 0;
-}
-
-__device__ __forceinline__ int pair_token(const ExpertLaunch& L, int p) {
-    return L.table != nullptr ? L.plan.pair_token[p] : p;
-}
 
 // ---------------------------------------------------------------------------
 // Phase A: gate/up.  Workgroup = 16 rows of gate and up of one expert, all
@@ -158,7 +45,7 @@ __global__ __launch_bounds__(256) void k_gate_up_rt(ExpertLaunch L) {
     typedef Mma<F16> M;
     typedef typename M::V V;
     Unit u;
-    if (!resolve_unit(L, kTileTok * MAXT, &u)) return;
+    if (!resolve_unit_rt(L, blockIdx.y, kTileTok * MAXT, &u)) return;
     const int H = u.e.hidden, I = u.e.inter;
     const int r0 = blockIdx.x * kTileRows;
     if (r0 >= I) return;
@@ -313,7 +200,7 @@ __global__ __launch_bounds__(256) void k_down_rt(ExpertLaunch L) {
     typedef Mma<false> M;
     typedef M::V V;
     Unit u;
-    if (!resolve_unit(L, kTileTok * MAXT, &u)) return;
+    if (!resolve_unit_rt(L, blockIdx.y, kTileTok * MAXT, &u)) return;
     const int H = u.e.hidden, I = u.e.inter;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int g = lane >> 4, c = lane & 15;
@@ -435,195 +322,12 @@ __global__ __launch_bounds__(256) void k_down_rt(ExpertLaunch L) {
 }
 
 // ---------------------------------------------------------------------------
-// Phase A with a compile-time trip count (the fast path at DeepSeek shapes).
-// NKB = k-blocks per wave (K split over the KS waves of the workgroup), D = k-blocks of weights
-// in flight per wave; every loop below is unrolled with constant bounds, so
-// the compiler keeps D stages of loads outstanding (exact vmcnt waits)
-// instead of draining the memory pipe every stage.
-// XLDS: the item's activation rows are staged once in LDS (np <= np_lds
-// rows, row stride hidden*2+16 bytes so the 16 token rows fall on different
-// banks); otherwise they ride the same prefetch ring from global memory.
-// Requires col blocks of 128 and row blocks multiple of 16 (fast_path_ok +
-// the template gate in launch_gate_up).
-template <int NKB, int D, int MAXT, bool F16, bool XLDS, int KS>
+// Phase A with a compile-time trip count: gate_up_tile (cx_gate_up.h) over
+// grid = (inter/16, items).
+template <int NKB, int D, int MAXT, bool F16, bool XLDS, int KS, bool SINGLE>
 __global__ __launch_bounds__(64 * KS) void k_gate_up_t(ExpertLaunch L) {
-    typedef Mma<F16> M;
-    typedef typename M::V V;
-    extern __shared__ __attribute__((aligned(16))) unsigned char xlds[];
-    Unit u;
-    if (!resolve_unit(L, kTileTok * MAXT, &u)) return;
-    const int H = u.e.hidden, I = u.e.inter;
-    const int r0 = blockIdx.x * kTileRows;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int g = lane >> 4, c = lane & 15;
-    const int kb0 = wave * NKB;
-
-    const size_t roff = (size_t)(r0 + c) * H + (size_t)kb0 * kKB + g * 32;
-    const uint8_t* pg = u.e.w_gate + roff;
-    const uint8_t* pu = u.e.w_up + roff;
-    const float* sg = u.e.s_gate + (size_t)(r0 / u.e.gate_rb) * (H / kKB) + kb0;
-    const float* su = u.e.s_up + (size_t)(r0 / u.e.up_rb) * (H / kKB) + kb0;
-    const int ntile = (u.np + kTileTok - 1) / kTileTok;
-    const size_t xs = (size_t)H * 2 + 16;  // LDS row stride in bytes
-    constexpr bool XRING = !XLDS && MAXT == 1;
-
-    // 1) weight prologue first: HBM latency is the long pole
-    u32x4 wb[D][4];
-#pragma unroll
-    for (int s = 0; s < D && s < NKB; ++s) {
-        wb[s][0] = ld16(pg + s * kKB);
-        wb[s][1] = ld16(pg + s * kKB + 16);
-        wb[s][2] = ld16(pu + s * kKB);
-        wb[s][3] = ld16(pu + s * kKB + 16);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    // 2) activations (L2) and scales
-    const unsigned char* xl = nullptr;
-    const uint16_t* xp[MAXT];
-    if (XLDS) {
-        // stage the np (<= 4) activation rows of this item: <= NKB 16-byte
-        // chunks per thread since hidden = NKB * KS * 128
-        const int n16 = H / 8;
-        const int total = u.np * n16;
-        u32x4 xr[NKB];
-#pragma unroll
-        for (int i = 0; i < NKB; ++i) {
-            const int idx = threadIdx.x + i * 64 * KS;
-            if (idx < total) {
-                const int q = idx / n16, j = idx - q * n16;
-                xr[i] = ld16(static_cast<const uint16_t*>(L.x) +
-                             (size_t)pair_token(L, u.pb + q) * H + j * 8);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < NKB; ++i) {
-            const int idx = threadIdx.x + i * 64 * KS;
-            if (idx < total) {
-                const int q = idx / n16, j = idx - q * n16;
-                *reinterpret_cast<u32x4*>(xlds + q * xs + j * 16) = xr[i];
-            }
-        }
-        xl = xlds + min(c, u.np - 1) * xs + ((size_t)kb0 * kKB + g * 32) * 2;
-    } else {
-#pragma unroll
-        for (int tt = 0; tt < MAXT; ++tt) {
-            const int q = min(tt * kTileTok + c, u.np - 1);
-            xp[tt] = static_cast<const uint16_t*>(L.x) + (size_t)pair_token(L, u.pb + q) * H +
-                     (size_t)kb0 * kKB + g * 32;
-        }
-    }
-    float scg[NKB], scu[NKB];
-#pragma unroll
-    for (int k = 0; k < NKB; ++k) {
-        scg[k] = ldf(sg + k);
-        scu[k] = ldf(su + k);
-    }
-    u32x4 xb[XRING ? D : 1][4];
-    if (XRING) {
-#pragma unroll
-        for (int s = 0; s < D && s < NKB; ++s) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) xb[s][j] = ld16(xp[0] + s * kKB + 8 * j);
-        }
-    }
-    if (XLDS) __syncthreads();
-
-    f32x4 accg[MAXT], accu[MAXT];
-#pragma unroll
-    for (int tt = 0; tt < MAXT; ++tt) {
-        accg[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        accu[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int k = 0; k < NKB; ++k) {
-        const int s = k % D;
-        V ag[4], au[4];
-        ag[0] = M::cvt(wb[s][0][0], wb[s][0][1]);
-        ag[1] = M::cvt(wb[s][0][2], wb[s][0][3]);
-        ag[2] = M::cvt(wb[s][1][0], wb[s][1][1]);
-        ag[3] = M::cvt(wb[s][1][2], wb[s][1][3]);
-        au[0] = M::cvt(wb[s][2][0], wb[s][2][1]);
-        au[1] = M::cvt(wb[s][2][2], wb[s][2][3]);
-        au[2] = M::cvt(wb[s][3][0], wb[s][3][1]);
-        au[3] = M::cvt(wb[s][3][2], wb[s][3][3]);
-#pragma unroll
-        for (int tt = 0; tt < MAXT; ++tt) {
-            if (MAXT == 1 || tt < ntile) {
-                V bx[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (XLDS) bx[j] = M::bits(*reinterpret_cast<const u32x4*>(xl + (k * kKB + 8 * j) * 2));
-                    else if (XRING) bx[j] = M::bits(xb[s][j]);
-                    else bx[j] = M::bits(ld16(xp[tt] + k * kKB + 8 * j));
-                }
-                f32x4 tg = M::mma(ag[0], bx[0], zero);
-                f32x4 tu = M::mma(au[0], bx[0], zero);
-#pragma unroll
-                for (int j = 1; j < 4; ++j) {
-                    tg = M::mma(ag[j], bx[j], tg);
-                    tu = M::mma(au[j], bx[j], tu);
-                }
-                accg[tt] += scg[k] * tg;
-                accu[tt] += scu[k] * tu;
-            }
-        }
-        if (k + D < NKB) {
-            // refill this stage right after its last use, D stages ahead
-            __builtin_amdgcn_sched_barrier(0);
-            const int kn = k + D;
-            wb[s][0] = ld16(pg + kn * kKB);
-            wb[s][1] = ld16(pg + kn * kKB + 16);
-            wb[s][2] = ld16(pu + kn * kKB);
-            wb[s][3] = ld16(pu + kn * kKB + 16);
-            if (XRING) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) xb[s][j] = ld16(xp[0] + kn * kKB + 8 * j);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-
-    __shared__ f32x4 red[KS][MAXT][2][64];
-#pragma unroll
-    for (int tt = 0; tt < MAXT; ++tt) {
-        red[wave][tt][0][lane] = accg[tt];
-        red[wave][tt][1][lane] = accu[tt];
-    }
-    __syncthreads();
-    for (int tt = wave; tt < ntile; tt += KS) {
-        f32x4 G = red[0][tt][0][lane], U = red[0][tt][1][lane];
-#pragma unroll
-        for (int w = 1; w < KS; ++w) {
-            G += red[w][tt][0][lane];
-            U += red[w][tt][1][lane];
-        }
-        const int q = tt * kTileTok + c;
-        if (q < u.np) {
-            const size_t p = (size_t)(u.pb + q);
-            const float wf = L.fold_weight ? L.plan.pair_weight[p] : 1.0f;
-            const int row = r0 + 4 * g;
-            uint32_t hi[4], lo[4];
-            float hv[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float gate = G[i], up = U[i];
-                const float h = (gate / (1.0f + expf(-gate))) * up;
-                hv[i] = h;
-                const float hw = h * wf;
-                hi[i] = bf16_rne(hw);
-                lo[i] = bf16_rne(hw - __uint_as_float(hi[i] << 16));
-            }
-            *reinterpret_cast<uint2*>(L.h_hi + p * I + row) =
-                uint2{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
-            *reinterpret_cast<uint2*>(L.h_lo + p * I + row) =
-                uint2{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
-            if (L.h_f32 != nullptr)
-                *reinterpret_cast<float4*>(L.h_f32 + p * I + row) = float4{hv[0], hv[1], hv[2], hv[3]};
-        }
-    }
+    extern __shared__ __attribute__((aligned(16))) unsigned char gu_lds[];
+    gate_up_tile<NKB, D, MAXT, F16, XLDS, KS, SINGLE>(L, blockIdx.x, blockIdx.y, gu_lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -634,7 +338,7 @@ __global__ __launch_bounds__(256) void k_down_t(ExpertLaunch L) {
     typedef Mma<false> M;
     typedef M::V V;
     Unit u;
-    if (!resolve_unit(L, kTileTok * MAXT, &u)) return;
+    if (!resolve_unit_rt(L, blockIdx.y, kTileTok * MAXT, &u)) return;
     const int H = u.e.hidden, I = u.e.inter;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int g = lane >> 4, c = lane & 15;
@@ -740,161 +444,11 @@ __global__ __launch_bounds__(256) void k_down_t(ExpertLaunch L) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode down projection with the weighted combine fused (T <= 16 tokens).
-// Workgroup = 16*RG output rows for every token; it walks every slot of the
-// plan (ascending expert id, shared expert last) and the KS waves split K
-// (NKBW k-blocks each).  MFMA column t holds w(t,s)*h(t,s) as hi+lo bf16
-// (written by phase A with the route weight folded in), or zero when token
-// t does not use slot s, so one fp32 accumulator tile per row tile sums every
-// expert's contribution in a fixed order.  Each wave drives RG row tiles
-// with the same B operand, so the h bytes delivered per weight byte drop by
-// RG (h is the MFMA operand every lane must receive, 4x the weight bytes of
-// a 16-row tile).  The weights ring prefetches across slot boundaries; past
-// the last slot it re-reads the last slot's lines (L2 hits).
-// grid = hidden/(16*RG), block = 64*KS.
-template <int NKBW, int KS, int RG>
-__global__ __launch_bounds__(64 * KS) void k_down_fused(ExpertLaunch L) {
-    typedef Mma<false> M;
-    typedef M::V V;
-    constexpr int NKB = NKBW * KS;  // k-blocks of one down row
-    const int n_slots = L.plan.hdr->n_slots;
-    const int H = L.hidden, I = L.inter;
-    const int r0 = blockIdx.x * kTileRows * RG;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int g = lane >> 4, c = lane & 15;
-    const int kb0 = wave * NKBW;
-    if (n_slots == 0) {  // nothing routed and no shared expert: y = 0
-        if (wave == 0 && c < L.n_tokens) {
-#pragma unroll
-            for (int q = 0; q < RG; ++q) {
-                const int row = r0 + q * kTileRows + 4 * g;
-                *reinterpret_cast<uint2*>(static_cast<uint16_t*>(L.y) + (size_t)c * H + row) = uint2{0u, 0u};
-                if (L.y_f32 != nullptr)
-                    *reinterpret_cast<float4*>(L.y_f32 + (size_t)c * H + row) = float4{0.f, 0.f, 0.f, 0.f};
-            }
-        }
-        return;
-    }
-    const size_t hoff = (size_t)kb0 * kKB + g * 32;
-    size_t woff[RG];
-#pragma unroll
-    for (int q = 0; q < RG; ++q) woff[q] = (size_t)(r0 + q * kTileRows + c) * I + (size_t)kb0 * kKB + g * 32;
-    // 1) slot 0's weights first (one dependent load: the slot record)
-    u32x4 wb[NKBW][RG][2];
-    {
-        const uint8_t* w0 = L.plan.slot_rec[0].w_down;
-#pragma unroll
-        for (int k = 0; k < NKBW; ++k) {
-#pragma unroll
-            for (int q = 0; q < RG; ++q) {
-                wb[k][q][0] = ld16(w0 + woff[q] + k * kKB);
-                wb[k][q][1] = ld16(w0 + woff[q] + k * kKB + 16);
-            }
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // 2) per-slot operands of this row block, staged once in LDS so the
-    //    streaming loop issues only weight and h loads, in order of use
-    extern __shared__ __attribute__((aligned(16))) unsigned char dlds[];
-    const uint8_t** s_w = reinterpret_cast<const uint8_t**>(dlds);                 // [n_slots]
-    float* s_sc = reinterpret_cast<float*>(dlds + 8 * (size_t)n_slots);            // [n_slots][NKB]
-    int* s_p = reinterpret_cast<int*>(s_sc + (size_t)n_slots * NKB);               // [n_slots][16]
-    for (int i = threadIdx.x; i < n_slots; i += 64 * KS) {
-        const SlotRec r = L.plan.slot_rec[i];
-        s_w[i] = r.w_down;
-        const float* sd = r.s_down + (size_t)(r0 / r.down_rb) * (I / kKB);
-        for (int k = 0; k < NKB; ++k) s_sc[i * NKB + k] = ldf(sd + k);
-    }
-    for (int i = threadIdx.x; i < n_slots * kTileTok; i += 64 * KS) s_p[i] = ldi(L.plan.slot_tok_pair + i);
-    __syncthreads();
-
-    u32x4 hb[8];
-    int p = s_p[c];
-    {
-        const uint16_t* hh = L.h_hi + (size_t)max(p, 0) * I + hoff;
-        const uint16_t* hl = L.h_lo + (size_t)max(p, 0) * I + hoff;
-        const u32x4 m = p >= 0 ? u32x4{~0u, ~0u, ~0u, ~0u} : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            hb[j] = ld16(hh + 8 * j) & m;
-            hb[4 + j] = ld16(hl + 8 * j) & m;
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    f32x4 acc[RG];
-#pragma unroll
-    for (int q = 0; q < RG; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < n_slots; ++s) {
-        const int sn = min(s + 1, n_slots - 1);
-        const uint8_t* pn = s_w[sn];   // past the last slot: same lines again (L2 hits)
-        const int pnext = s + 1 < n_slots ? s_p[sn * kTileTok + c] : -1;
-#pragma unroll
-        for (int k = 0; k < NKBW; ++k) {
-            V bh[4], bl[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                bh[j] = M::bits(hb[j]);
-                bl[j] = M::bits(hb[4 + j]);
-            }
-            const float sc = s_sc[s * NKB + kb0 + k];
-#pragma unroll
-            for (int q = 0; q < RG; ++q) {
-                V a[4];
-                a[0] = M::cvt(wb[k][q][0][0], wb[k][q][0][1]);
-                a[1] = M::cvt(wb[k][q][0][2], wb[k][q][0][3]);
-                a[2] = M::cvt(wb[k][q][1][0], wb[k][q][1][1]);
-                a[3] = M::cvt(wb[k][q][1][2], wb[k][q][1][3]);
-                f32x4 t = M::mma(a[0], bh[0], zero);
-                t = M::mma(a[0], bl[0], t);
-#pragma unroll
-                for (int j = 1; j < 4; ++j) {
-                    t = M::mma(a[j], bh[j], t);
-                    t = M::mma(a[j], bl[j], t);
-                }
-                acc[q] += sc * t;
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            // next step's h first (needed soonest), then this stage's refill;
-            // unconditional loads (absent pairs read pair 0) masked to zero:
-            // no branch, so the waits stay exact
-            const int pq = k + 1 < NKBW ? p : pnext;
-            const int kq = k + 1 < NKBW ? k + 1 : 0;
-            const uint16_t* hh = L.h_hi + (size_t)max(pq, 0) * I + hoff + kq * kKB;
-            const uint16_t* hl = L.h_lo + (size_t)max(pq, 0) * I + hoff + kq * kKB;
-            const u32x4 mq = pq >= 0 ? u32x4{~0u, ~0u, ~0u, ~0u} : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                hb[j] = ld16(hh + 8 * j) & mq;
-                hb[4 + j] = ld16(hl + 8 * j) & mq;
-            }
-#pragma unroll
-            for (int q = 0; q < RG; ++q) {
-                wb[k][q][0] = ld16(pn + woff[q] + k * kKB);
-                wb[k][q][1] = ld16(pn + woff[q] + k * kKB + 16);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        p = pnext;
-    }
-    __shared__ f32x4 red[KS][RG][64];
-#pragma unroll
-    for (int q = 0; q < RG; ++q) red[wave][q][lane] = acc[q];
-    __syncthreads();
-    for (int q = wave; q < RG; q += KS) {
-        if (c < L.n_tokens) {
-            f32x4 v = red[0][q][lane];
-#pragma unroll
-            for (int w = 1; w < KS; ++w) v += red[w][q][lane];
-            const int row = r0 + q * kTileRows + 4 * g;
-            uint16_t* yo = static_cast<uint16_t*>(L.y) + (size_t)c * H + row;
-            *reinterpret_cast<uint2*>(yo) =
-                uint2{cast_out(v[0], L.out_dtype) | (cast_out(v[1], L.out_dtype) << 16),
-                      cast_out(v[2], L.out_dtype) | (cast_out(v[3], L.out_dtype) << 16)};
-            if (L.y_f32 != nullptr)
-                *reinterpret_cast<float4*>(L.y_f32 + (size_t)c * H + row) = float4{v[0], v[1], v[2], v[3]};
-        }
-    }
+// Down projection per work item of <= 16 pairs: down_item_tile (cx_down.h),
+// grid = (hidden/64, items).
+template <int NKB, int D, bool SINGLE, bool XL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XL ? 4 : 2))) void k_down_item(ExpertLaunch L) {
+    down_item_tile<NKB, D, SINGLE, XL>(L, blockIdx.x, blockIdx.y);
 }
 
 // ---------------------------------------------------------------------------
@@ -937,6 +491,56 @@ __global__ __launch_bounds__(256) void k_combine(PlanPtrs plan, const float* __r
     if (y_f32 != nullptr) {
         *reinterpret_cast<float4*>(y_f32 + (size_t)t * hidden + f) = float4{acc[0], acc[1], acc[2], acc[3]};
     }
+}
+
+// Decode combine: the y_part row of (token t, route k) is S0 + t*K + k (S0 =
+// T with a shared expert, whose rows are [0, T)), so the route weights, the
+// pair table and the partial rows are all fetched at once (one round trip);
+// a route dropped by the planner (pair -1) contributes nothing.  Same order
+// as k_combine: route order, shared expert last.
+__global__ __launch_bounds__(256) void k_combine_dec(const int* __restrict__ token_pairs,
+                                                     const float* __restrict__ topk_w,
+                                                     const float* __restrict__ y_part, int n_tokens,
+                                                     int top_k, int has_shared, int hidden, void* y,
+                                                     int out_dtype, float* y_f32) {
+    constexpr int KC = 8;  // routes fetched per batch
+    const int n4 = hidden / 4;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n_tokens * n4) return;
+    const int t = idx / n4;
+    const int f = (idx - t * n4) * 4;
+    const int s0 = has_shared ? n_tokens : 0;
+    const int* tp = token_pairs + (size_t)t * (top_k + 1);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < top_k; k0 += KC) {
+        int p[KC];
+        float w[KC];
+        float4 v[KC];
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            const int k = min(k0 + j, top_k - 1);
+            p[j] = k0 + j < top_k ? tp[k] : -1;
+            w[j] = topk_w[(size_t)t * top_k + k];
+            v[j] = *reinterpret_cast<const float4*>(y_part + ((size_t)s0 + (size_t)t * top_k + k) * hidden + f);
+        }
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            if (p[j] >= 0) {
+                acc[0] += w[j] * v[j].x;
+                acc[1] += w[j] * v[j].y;
+                acc[2] += w[j] * v[j].z;
+                acc[3] += w[j] * v[j].w;
+            }
+        }
+    }
+    if (tp[top_k] >= 0) {
+        const float4 v = *reinterpret_cast<const float4*>(y_part + (size_t)t * hidden + f);
+        acc[0] += v.x;
+        acc[1] += v.y;
+        acc[2] += v.z;
+        acc[3] += v.w;
+    }
+    store_out4(y, y_f32, (size_t)t * hidden + f, acc, out_dtype);
 }
 
 // ---------------------------------------------------------------------------
@@ -1008,53 +612,63 @@ int env_int(const char* name, int dflt) {
     return v ? std::atoi(v) : dflt;
 }
 
-// Waves per workgroup of the gate/up kernel (K split) at hidden = 7168; the
-// default comes from the measured sweep (CX_GU_KS overrides: 2, 4 or 8).
-int gate_up_ks() {
-    static const int ks = env_int("CX_GU_KS", 4);
-    return ks;
-}
-
-int down_fused_ks() {
-    static const int ks = env_int("CX_DN_KS", 8);
-    return ks;
-}
-
 template <int NKB, int KS, int MAXT, bool F16>
 void go_gate_up(const ExpertLaunch& L, dim3 grid, hipStream_t s) {
     constexpr int D = NKB < 4 ? NKB : 4;
+    const dim3 block(64 * KS);
+    const bool single = L.table == nullptr;
     if (MAXT == 1 && L.np_lds > 0) {
-        const size_t lds = (size_t)L.np_lds * ((size_t)L.hidden * 2 + 16);
-        cx_launch((k_gate_up_t<NKB, D, MAXT, F16, true, KS>), grid, dim3(64 * KS), lds, s, L);
+        const size_t lds = gate_up_lds_bytes(KS, 1, L.np_lds, L.hidden);
+        if (single) cx_launch((k_gate_up_t<NKB, D, 1, F16, true, KS, true>), grid, block, lds, s, L);
+        else cx_launch((k_gate_up_t<NKB, D, 1, F16, true, KS, false>), grid, block, lds, s, L);
     } else {
-        cx_launch((k_gate_up_t<NKB, D, MAXT, F16, false, KS>), grid, dim3(64 * KS), 0, s, L);
+        const size_t lds = gate_up_lds_bytes(KS, MAXT, 0, L.hidden);
+        if (single) cx_launch((k_gate_up_t<NKB, D, MAXT, F16, false, KS, true>), grid, block, lds, s, L);
+        else cx_launch((k_gate_up_t<NKB, D, MAXT, F16, false, KS, false>), grid, block, lds, s, L);
     }
 }
 
 template <int MAXT, bool F16>
 bool pick_gate_up(const ExpertLaunch& L, dim3 grid, hipStream_t s) {
     if (L.hidden % kKB != 0) return false;
-    const int nkb = L.hidden / kKB;
-    if (nkb == 56) {
-        if (MAXT != 1) {  // the KS x MAXT reduction tile must stay within LDS
-            go_gate_up<14, 4, MAXT, F16>(L, grid, s);
-            return true;
-        }
-        switch (gate_up_ks()) {
-            case 2: go_gate_up<28, 2, MAXT, F16>(L, grid, s); return true;
-            case 8: go_gate_up<7, 8, MAXT, F16>(L, grid, s); return true;
-            default: go_gate_up<14, 4, MAXT, F16>(L, grid, s); return true;
-        }
-    }
-    switch (nkb) {
+    switch (L.hidden / kKB) {
+        case 56: go_gate_up<14, 4, MAXT, F16>(L, grid, s); return true;
         case 4: go_gate_up<1, 4, MAXT, F16>(L, grid, s); return true;
         case 8: go_gate_up<2, 4, MAXT, F16>(L, grid, s); return true;
         default: return false;
     }
 }
 
+// Weight ring depth of the LDS-staged down kernel: 6 k-blocks (12 KB) in
+// flight per wave keeps it within 128 registers (4 waves per SIMD, so a
+// decode grid of 8 experts x 112 tiles is resident at once).
+constexpr int kDownXlDepth = 6;
+
+// XL (h staged in LDS) when every item holds <= 4 pairs: at most 4 tokens
+// (np_lds_down set by the caller), else h rides the weight ring.
+template <int NKB>
+void go_down_item(const ExpertLaunch& L, dim3 grid, hipStream_t s) {
+    const bool single = L.table == nullptr;
+    const bool xl = L.n_tokens <= kDownLdsRows;
+    const size_t lds = xl ? down_item_lds(L.inter) : 0;
+    if (xl) {
+        if (single) cx_launch((k_down_item<NKB, kDownXlDepth, true, true>), grid, dim3(256), lds, s, L);
+        else cx_launch((k_down_item<NKB, kDownXlDepth, false, true>), grid, dim3(256), lds, s, L);
+    } else {
+        if (single) cx_launch((k_down_item<NKB, 4, true, false>), grid, dim3(256), 0, s, L);
+        else cx_launch((k_down_item<NKB, 4, false, false>), grid, dim3(256), 0, s, L);
+    }
+}
+
 template <int MAXT>
 bool pick_down(const ExpertLaunch& L, dim3 grid, hipStream_t s) {
+    if (MAXT == 1) {
+        switch (L.inter / kKB) {
+            case 4: go_down_item<4>(L, grid, s); return true;
+            case 16: go_down_item<16>(L, grid, s); return true;
+            default: return false;
+        }
+    }
     switch (L.inter / kKB) {
         case 4: cx_launch((k_down_t<4, 4, MAXT>), grid, dim3(256), 0, s, L); return true;
         case 16: cx_launch((k_down_t<16, 4, MAXT>), grid, dim3(256), 0, s, L); return true;
@@ -1096,54 +710,20 @@ hipError_t launch_down(const ExpertLaunch& L, hipStream_t s) {
     return hipGetLastError();
 }
 
-bool down_fused_ok(int inter) { return inter == 2048 || inter == 512; }
-
-// Row tiles per wave of the fused down kernel (CX_DN_RG overrides: 1, 2, 4).
-int down_fused_rg() {
-    static const int rg = env_int("CX_DN_RG", 2);
-    return rg;
-}
-
-template <int NKBW, int KS, int RG>
-void go_down_fused(const ExpertLaunch& L, size_t lds, hipStream_t s) {
-    cx_launch((k_down_fused<NKBW, KS, RG>), dim3(L.hidden / (kTileRows * RG)), dim3(64 * KS),
-                       lds, s, L);
-}
-
-template <int NKBW, int KS>
-void pick_down_rg(const ExpertLaunch& L, size_t lds, hipStream_t s) {
-    int rg = down_fused_rg();
-    if (rg != 2 && rg != 4) rg = 1;
-    if (L.hidden % (kTileRows * rg) != 0) rg = 1;  // grid = hidden / (16 * rg) row groups
-    switch (rg) {
-        case 2: go_down_fused<NKBW, KS, 2>(L, lds, s); break;
-        case 4: go_down_fused<NKBW, KS, 4>(L, lds, s); break;
-        default: go_down_fused<NKBW, KS, 1>(L, lds, s); break;
-    }
-}
-
-hipError_t launch_down_fused(const ExpertLaunch& L, int max_slots, hipStream_t s) {
-    const int nkb = L.inter / kKB;
-    const size_t lds = (size_t)max_slots * (8 + 4 * nkb + 4 * kTileTok);
-    if (nkb == 16) {
-        switch (down_fused_ks()) {
-            case 8: pick_down_rg<2, 8>(L, lds, s); break;
-            case 16: pick_down_rg<1, 16>(L, lds, s); break;
-            default: pick_down_rg<4, 4>(L, lds, s); break;
-        }
-    } else if (nkb == 4) {
-        pick_down_rg<1, 4>(L, lds, s);
-    } else {
-        return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
-
 hipError_t launch_combine(const PlanPtrs& plan, const float* y_part, int n_tokens, int top_k,
                           int hidden, void* y, int out_dtype, float* y_f32, hipStream_t s) {
     const int n = n_tokens * (hidden / 4);
     cx_launch(k_combine, dim3((n + 255) / 256), dim3(256), 0, s, plan, y_part,
                        n_tokens, top_k, hidden, y, out_dtype, y_f32);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine_dec(const PlanPtrs& plan, const float* topk_w, const float* y_part,
+                              int n_tokens, int top_k, int has_shared, int hidden, void* y,
+                              int out_dtype, float* y_f32, hipStream_t s) {
+    const int n = n_tokens * (hidden / 4);
+    cx_launch(k_combine_dec, dim3((n + 255) / 256), dim3(256), 0, s, plan.token_pairs, topk_w,
+              y_part, n_tokens, top_k, has_shared, hidden, y, out_dtype, y_f32);
     return hipGetLastError();
 }
 

@@ -30,14 +30,20 @@ constexpr int kWaves = 4;       // waves per workgroup
 // Grouped-execution plan, built on the device by k_plan from (topk_ids,
 // topk_w) and consumed by the gate/up, down and combine kernels.
 //   slot   : one active expert (ascending expert id), the shared expert last
-//   pair   : one (token, expert) assignment, grouped by slot
-//   item   : a run of <= item_cap pairs of one slot (one grouped work unit)
+//   pair   : one (token, expert) assignment, grouped by slot.  The shared
+//            expert's pairs are [0, T) (pair t = token t), so its h can be
+//            produced before the routing is known; routed pairs follow.
+//   item   : a run of <= item_cap pairs of one slot (one grouped work unit);
+//            routed items first, the shared expert's items last
 struct PlanHdr {
     int n_slots;
     int n_items;
     int n_pairs;
-    int pad;
+    int n_routed_slots;  // slots [0, n_routed_slots) are routed experts
+    int n_routed_items;  // items [0, n_routed_items) belong to routed slots
+    int pad[3];
 };
+constexpr int kPlanHdrInts = 8;
 
 // Flat per-item / per-slot records written by the planner, so a workgroup
 // reaches its weight pointers with one dependent load.
@@ -50,6 +56,7 @@ struct ItemRec {
     const float* s_down;
     int pb, np;            // pair range
     int up_rb, gate_rb, down_rb, pad;
+    int tok[4];            // tokens of the item's first (up to) 4 pairs
 };
 
 struct SlotRec {
@@ -72,7 +79,9 @@ struct PlanPtrs {
     int* pair_token;       // [max_pairs]
     float* pair_weight;    // [max_pairs]
     int* token_pairs;      // [T * (K+1)], pair index or -1 (shared in column K)
-    int* slot_tok_pair;    // [max_slots * 16] pair of (slot, token) or -1; T <= 16 only (nullable)
+    int* pair_row;         // [max_pairs] y_part row of a pair: t for the shared expert's,
+                           // T + t*K + k for (token t, route k); decode plans only (nullable:
+                           // row = pair)
 };
 
 // Device error bits (ORed into the context's flag, read by cx_ctx_sync).
@@ -130,15 +139,21 @@ struct ExpertLaunch {
     int out_dtype;
     int fold_weight;              // phase A multiplies h by the pair's route weight
     int np_lds;                   // >0: stage up to np_lds activation rows per item in LDS
+    int skip_shared;              // grouped mode: routed items only (shared expert done apart)
 };
 
 hipError_t launch_gate_up(const ExpertLaunch& L, hipStream_t s);
+// Down projection per work item: grouped mode writes fp32 y_part[pair]
+// (combined afterwards by launch_combine), single mode writes y / y_f32.
 hipError_t launch_down(const ExpertLaunch& L, hipStream_t s);
-bool down_fused_ok(int inter);
-hipError_t launch_down_fused(const ExpertLaunch& L, int max_slots, hipStream_t s);
 hipError_t launch_combine(const PlanPtrs& plan, const float* y_part, int n_tokens,
                           int top_k, int hidden, void* y, int out_dtype, float* y_f32,
                           hipStream_t s);
+// Combine of a decode plan (y_part rows by pair_row): weights read straight
+// from the routes, every load independent of the others.
+hipError_t launch_combine_dec(const PlanPtrs& plan, const float* topk_w, const float* y_part,
+                              int n_tokens, int top_k, int has_shared, int hidden, void* y,
+                              int out_dtype, float* y_f32, hipStream_t s);
 hipError_t launch_plan(const int32_t* ids, const float* w, int n_tokens, int top_k,
                        const cx_expert_desc* table, int n_experts, int has_shared,
                        int item_cap, int max_items, PlanPtrs plan, int* err_flag,
@@ -170,6 +185,25 @@ struct RouteArgs {
 };
 hipError_t launch_route(const RouteArgs& r, hipStream_t s);
 int route_max_experts();
+
+// Decode pipeline for T <= 16 tokens, E <= 256 experts.
+//  cx_moe_layer:  stage 1 = router logits;
+//                 stage 2 = selection + planner beside the shared expert's
+//                 gate/up (sg nullable: no shared expert).
+//  cx_moe_decode: planner from given routes beside the shared expert's gate/up.
+// The shared-expert launch is a single-mode ExpertLaunch record whose pairs
+// are the tokens (pair t = token t, the plan's shared pairs).
+bool dec_route_ok(int n_experts, int n_group);
+bool dec_shared_ok(int hidden, int inter);
+// Activation rows the shared expert's gate/up tiles of stage 2 stage in LDS
+// (0: stream them from L2).
+int dec_sgu_np_lds(int hidden, int n_tokens, int max_lds);
+hipError_t launch_dec_logits(const RouteArgs& r, hipStream_t s);
+hipError_t launch_dec_select_sgu(const RouteArgs& r, const ExpertLaunch* sg, hipStream_t s);
+hipError_t launch_dec_plan_sgu(const int32_t* ids, const float* w, int n_tokens, int top_k,
+                               const cx_expert_desc* table, int n_experts, int has_shared,
+                               PlanPtrs plan, int* err_flag, const ExpertLaunch* sg,
+                               hipStream_t s);
 
 // Upload helpers / generator.
 hipError_t launch_canonicalize_fp8(uint8_t* p, uint64_t n, hipStream_t s);

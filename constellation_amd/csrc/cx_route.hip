@@ -1,4 +1,5 @@
-// cx_route.hip — DeepSeek-V3 router and the grouped-execution planner.
+// cx_route.hip — DeepSeek-V3 router, the grouped-execution planners, and the
+// decode-pipeline stages that run the shared expert beside them.
 //
 // Router semantics: route_token_real (server/moe_layer_runtime.py:232-408);
 // the HF twin is MoEGate.forward (tmp/patched_modeling/
@@ -6,26 +7,38 @@
 // fp64 and the whole selection runs in fp64, so the chosen expert sets equal
 // the exact-math decision; ties break toward the lower index.
 //
-// Launch shapes: k_route_logits (one workgroup per expert row streams W_r
-// once for up to 16 tokens), then
-//  * T <= 16: k_route_select_plan — one workgroup selects every token (one
-//    wave per token) and, for cx_moe_layer, builds the grouped plan;
-//  * T > 16: k_route_select (one wave per token), then k_plan.
-#include "cx_internal.h"
+// Launch shapes
+//  * cx_route / general path: k_route_logits (one workgroup per expert row
+//    streams W_r once for up to 16 tokens), then k_route_select_small
+//    (T <= 16, one workgroup) or k_route_select (4 tokens per workgroup),
+//    then, for the grouped MoE, k_plan.
+//  * decode pipeline (T <= 16, E <= 256):
+//      stage 1  k_dec_logits        router logits
+//      stage 2  k_dec_select_sgu    selection + planner (workgroup 0) |
+//                                   shared expert gate/up tiles
+//    or, with routes given (cx_moe_decode),
+//      stage 2' k_dec_plan_sgu      planner (workgroup 0) | shared gate/up.
+//    The selection and planner are a latency-bound single workgroup; the
+//    shared expert's gate/up (29 MB of weights) streams from HBM on the
+//    otherwise idle CUs meanwhile (its down projection joins the routed
+//    experts' down launch).
+#include <algorithm>
+
+#include "cx_down.h"
+#include "cx_gate_up.h"
 
 namespace cx {
 namespace {
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
 constexpr int kRouteThreads = 256;
 constexpr int kRouteTB = 16;        // tokens per row workgroup
 constexpr int kMaxRouteExperts = 1024;
+constexpr int kDecMaxExperts = 256;  // decode planner: one thread per expert
+constexpr int kDecThreads = 1024;    // stage-2 workgroup: 16 selection waves
 
 __device__ __forceinline__ bool better(double a, int ia, double b, int ib) {
     return a > b || (a == b && ia < ib);
 }
-
 
 // Raw 8-element chunk of bf16 (one dwordx4) or fp32 (two dwordx4) values,
 // widened to fp64 at use (products of bf16 or fp32 values are exact in fp64).
@@ -35,10 +48,10 @@ struct Chunk8 {
     __device__ __forceinline__ void load(const void* base, size_t elem) {
         if (F32) {
             const float* p = static_cast<const float*>(base) + elem;
-            a = *reinterpret_cast<const u32x4*>(p);
-            b = *reinterpret_cast<const u32x4*>(p + 4);
+            a = ld16(p);
+            b = ld16(p + 4);
         } else {
-            a = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + elem);
+            a = ld16(static_cast<const uint16_t*>(base) + elem);
         }
     }
     __device__ __forceinline__ double get(int i) const {
@@ -54,7 +67,7 @@ struct Chunk8 {
 // of a pass are issued before any FMA, and activations are fetched for 4
 // tokens at a time (one L2 round trip per group of tokens).
 template <bool XF32, bool WF32>
-__device__ void row_logits(const void* __restrict__ x, const void* __restrict__ w, int t0, int nt,
+__device__ __forceinline__ void row_logits(const void* __restrict__ x, const void* __restrict__ w, int t0, int nt,
                            int hidden, int n_experts, double* __restrict__ logits,
                            double* red /* [4][kRouteTB] */) {
     const int e = blockIdx.x;
@@ -77,11 +90,13 @@ __device__ void row_logits(const void* __restrict__ x, const void* __restrict__ 
                 Chunk8<XF32> xc[4][G];
 #pragma unroll
                 for (int tt = 0; tt < 4; ++tt) {
-                    const int t = min(tg * 4 + tt, nt - 1);
+                    if (tg * 4 + tt < nt) {
 #pragma unroll
-                    for (int j = 0; j < G; ++j) {
-                        const int ci = c0 + j * kRouteThreads + tid;
-                        if (ci < nchunk) xc[tt][j].load(x, (size_t)(t0 + t) * hidden + (size_t)ci * 8);
+                        for (int j = 0; j < G; ++j) {
+                            const int ci = c0 + j * kRouteThreads + tid;
+                            if (ci < nchunk)
+                                xc[tt][j].load(x, (size_t)(t0 + tg * 4 + tt) * hidden + (size_t)ci * 8);
+                        }
                     }
                 }
 #pragma unroll
@@ -118,9 +133,93 @@ __device__ void row_logits(const void* __restrict__ x, const void* __restrict__ 
     }
 }
 
+// Decode form of row_logits: expert row e, tokens [t0, t0 + nt), nt <= 4,
+// with the accumulators and the raw activation chunks of one pass held in
+// few registers (the kernel shares its register budget with the shared
+// expert's gate/up tiles).  bf16 weights: the product of two bf16 values is
+// exact in fp32, so acc + (double)(w*x) rounds exactly like fma(w, x, acc)
+// in fp64; fp32 weights use the fp64 fma.  Same fixed summation order.
+__device__ __forceinline__ float bf16_at(u32x4 v, int i) {
+    const uint32_t w = v[i >> 1];
+    return __uint_as_float((i & 1) ? (w & 0xFFFF0000u) : (w << 16));
+}
+
+template <bool WF32, int NT>
+__device__ __forceinline__ void row_logits4(const void* __restrict__ x, const void* __restrict__ w,
+                                            int e, int t0, int nt, int hidden, int n_experts,
+                                            double* __restrict__ logits,
+                                            double* red /* [NT/64][4] */) {
+    constexpr int NW = NT / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    const int nchunk = hidden / 8;
+    constexpr int G = NT >= 512 ? 2 : 4;
+    for (int c0 = 0; c0 < nchunk; c0 += G * NT) {
+        u32x4 wr[G][WF32 ? 2 : 1];
+        u32x4 xr[4][G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const int ci = c0 + j * NT + tid;
+            if (ci < nchunk) {
+                if (WF32) {
+                    const float* p = static_cast<const float*>(w) + (size_t)e * hidden + (size_t)ci * 8;
+                    wr[j][0] = ld16(p);
+                    wr[j][WF32 ? 1 : 0] = ld16(p + 4);
+                } else {
+                    wr[j][0] = ld16(static_cast<const uint16_t*>(w) + (size_t)e * hidden + (size_t)ci * 8);
+                }
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+            for (int j = 0; j < G; ++j) {
+                const int ci = c0 + j * NT + tid;
+                if (tt < nt && ci < nchunk)
+                    xr[tt][j] = ld16(static_cast<const uint16_t*>(x) + (size_t)(t0 + tt) * hidden + (size_t)ci * 8);
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+            for (int j = 0; j < G; ++j) {
+                const int ci = c0 + j * NT + tid;
+                if (tt < nt && ci < nchunk) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const float wf = WF32 ? __uint_as_float(wr[j][WF32 ? (i >> 2) : 0][i & 3])
+                                              : bf16_at(wr[j][0], i);
+                        const float xf = bf16_at(xr[tt][j], i);
+                        if (WF32) acc[tt] = fma(static_cast<double>(wf), static_cast<double>(xf), acc[tt]);
+                        else acc[tt] = acc[tt] + static_cast<double>(wf * xf);
+                    }
+                }
+                // bounded live ranges: one chunk's conversions at a time
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        if (t < nt) {
+            double v = acc[t];
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+            if (lane == 0) red[wave * 4 + t] = v;
+        }
+    }
+    __syncthreads();
+    if (tid < nt) {
+        double v = red[tid];
+#pragma unroll
+        for (int w2 = 1; w2 < NW; ++w2) v += red[w2 * 4 + tid];
+        logits[(size_t)(t0 + tid) * n_experts + e] = v;
+    }
+}
+
 // Selection for one token by one wave.  c / taken are this wave's LDS
-// scratch of n_experts entries.
-__device__ void select_token(const double* __restrict__ lrow, const float* __restrict__ bias,
+// scratch of n_experts entries (any expert count; the fallback).
+__device__ __forceinline__ void select_token(const double* __restrict__ lrow, const float* __restrict__ bias,
                              const uint8_t* __restrict__ resident, int n_experts, int n_group,
                              int topk_group, int top_k, int norm, float scale,
                              int32_t* __restrict__ ids, float* __restrict__ wout, double* c,
@@ -201,13 +300,13 @@ __device__ void select_token(const double* __restrict__ lrow, const float* __res
     }
 }
 
+// ---------------------------------------------------------------------------
 // Register-resident selection (one wave per token): lane l owns the EPL
 // consecutive experts [l*EPL, (l+1)*EPL); a group of epg experts is a
 // segment of LPG = epg/EPL lanes (a power of two <= 16, so a group never
 // crosses a 16-lane DPP row).  Same decisions, tie rules and fixed
 // summation order as select_token.  Cross-lane steps use DPP moves
-// (row_shr, row_bcast) instead of ds_bpermute shuffles, so one arg-max costs
-// a few dozen VALU cycles rather than a chain of LDS-crossbar round trips.
+// (row_shr, row_bcast) instead of ds_bpermute shuffles.
 struct Top2 {
     double v1, v2;
     int i1, i2;
@@ -286,31 +385,88 @@ __device__ __forceinline__ double readlane_d(double v, int lane) {
     return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned>(lo));
 }
 
+// Sigmoid score s and choice score c of one expert for one token, the
+// reference's steps (moe_layer_runtime.py:323-341): s = sigmoid(logit),
+// c = s + e_score_correction_bias; a non-resident expert gets c = -inf and
+// s = 0.
+__device__ __forceinline__ void expert_scores(double logit, float bias, bool res, double* s,
+                                              double* c) {
+    const double sg = 1.0 / (1.0 + exp(-logit));
+    *s = res ? sg : 0.0;
+    *c = res ? sg + static_cast<double>(bias) : -INFINITY;
+}
+
+// Inputs of one token's selection, held by its wave (EPL experts per lane),
+// and the number of resident experts.
 template <int EPL>
-__device__ void select_token_reg(const double* __restrict__ lrow, const float* __restrict__ bias,
-                                 const uint8_t* __restrict__ resident, int n_experts, int n_group,
-                                 int topk_group, int top_k, int norm, float scale,
-                                 int32_t* __restrict__ ids, float* __restrict__ wout) {
+struct SelIn {
+    double s[EPL], c[EPL];
+    int nres;
+};
+
+template <int EPL>
+__device__ __forceinline__ void sel_load(SelIn<EPL>& in, const double* __restrict__ lrow,
+                                         const float* __restrict__ bias,
+                                         const uint8_t* __restrict__ resident) {
+    const int base = (threadIdx.x & 63) * EPL;
+    in.nres = 0;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+        const bool res = resident == nullptr || resident[base + i] != 0;
+        expert_scores(lrow[base + i], bias[base + i], res, &in.s[i], &in.c[i]);
+        in.nres += __popcll(__ballot(res));
+    }
+}
+
+// From scores already in LDS (row of E doubles each) and the residency count.
+template <int EPL>
+__device__ __forceinline__ void sel_load_lds(SelIn<EPL>& in, const double* s_row, const double* c_row,
+                                             int nres) {
+    const int base = (threadIdx.x & 63) * EPL;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+        in.s[i] = s_row[base + i];
+        in.c[i] = c_row[base + i];
+    }
+    in.nres = nres;
+}
+
+// Lane r < kk holds pick r of the token (expert, final weight);
+// kk = min(top_k, #resident).
+struct SelOut {
+    int isel;
+    float w;
+    int kk;
+};
+
+// Sigmoid scores, choice scores and the group stage (top-2 sum per group,
+// topk_group groups kept; candidates of the other groups become -inf), exact
+// in fp64.  Shared by the exact and the fast top-k stages.
+template <int EPL>
+struct SelState {
+    double s[EPL], c[EPL];
+    int nres;
+};
+
+template <int EPL>
+__device__ __forceinline__ SelState<EPL> sel_groups(const SelIn<EPL>& in, int n_experts,
+                                                    int n_group, int topk_group) {
     const int lane = threadIdx.x & 63;
     const int base = lane * EPL;
     const int epg = n_experts / n_group;
     const int lpg = epg / EPL;  // lanes per group: power of two <= 16 (host-checked)
-    double s[EPL], c[EPL];
-    int nres = 0;
+    SelState<EPL> st;
+    st.nres = in.nres;
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
-        const int e = base + i;
-        const double sg = 1.0 / (1.0 + exp(-lrow[e]));
-        const bool res = resident == nullptr || resident[e] != 0;
-        s[i] = res ? sg : 0.0;
-        c[i] = res ? sg + static_cast<double>(bias[e]) : -INFINITY;
-        nres += __popcll(__ballot(res));
+        st.s[i] = in.s[i];
+        st.c[i] = in.c[i];
     }
     // group score: top-2 sum over the group's lane segment, complete in the
     // segment's last lane
     Top2 t{-INFINITY, -INFINITY, kNoIdx, kNoIdx};
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) t = merge2(t, Top2{c[i], -INFINITY, base + i, kNoIdx});
+    for (int i = 0; i < EPL; ++i) t = merge2(t, Top2{st.c[i], -INFINITY, base + i, kNoIdx});
     const int sub = lane & (lpg - 1);
     if (lpg > 1) top2_step<0x111>(t, sub >= 1);
     if (lpg > 2) top2_step<0x112>(t, sub >= 2);
@@ -318,22 +474,34 @@ __device__ void select_token_reg(const double* __restrict__ lrow, const float* _
     if (lpg > 8) top2_step<0x118>(t, sub >= 8);
     const double gs_lane = epg >= 2 ? t.v1 + t.v2 : t.v1;
     const int grp = base / epg;
-    // the full group scores sit in each segment's last lane: read them all
-    // (uniform lane index) and rank this lane's group among them
+    // the full group scores sit in each segment's last lane: this lane's own
+    // by one cross-lane read, the others as uniform values; rank this lane's
+    // group among them
+    const int src = grp * lpg + lpg - 1;
+    const long long gb = __double_as_longlong(gs_lane);
+    const int glo = __shfl(static_cast<int>(gb), src, 64), ghi = __shfl(static_cast<int>(gb >> 32), src, 64);
+    const double my_gs = __longlong_as_double((static_cast<long long>(ghi) << 32) | static_cast<unsigned>(glo));
     int rank = 0;
-    double my_gs = 0.0;
-    for (int g2 = 0; g2 < n_group; ++g2) {
-        const double o = readlane_d(gs_lane, g2 * lpg + lpg - 1);
-        if (g2 == grp) my_gs = o;
-    }
     for (int g2 = 0; g2 < n_group; ++g2) {
         const double o = readlane_d(gs_lane, g2 * lpg + lpg - 1);
         if (g2 != grp && better(o, g2, my_gs, grp)) ++rank;
     }
     if (rank >= topk_group) {
 #pragma unroll
-        for (int i = 0; i < EPL; ++i) c[i] = -INFINITY;
+        for (int i = 0; i < EPL; ++i) st.c[i] = -INFINITY;
     }
+    return st;
+}
+
+template <int EPL>
+__device__ __forceinline__ SelOut select_reg(const SelIn<EPL>& in, int n_experts, int n_group,
+                                             int topk_group, int top_k, int norm, float scale) {
+    const int lane = threadIdx.x & 63;
+    const int base = lane * EPL;
+    SelState<EPL> st = sel_groups<EPL>(in, n_experts, n_group, topk_group);
+    double* s = st.s;
+    double* c = st.c;
+    const int nres = st.nres;
     const int k = min(top_k, nres);
     unsigned taken = 0;
     double wsum = 0.0, wsel = 0.0;
@@ -360,23 +528,120 @@ __device__ void select_token_reg(const double* __restrict__ lrow, const float* _
         if (lane == r) { isel = bi; wsel = sv; }
         wsum += sv;
     }
+    // normalise in pick order on every lane (same fixed order as the oracle)
     const double d = wsum + 1e-20;
-    if (lane < top_k) {
-        if (lane < k) {
-            double v = wsel;
-            if (norm && k > 1) v /= d;
-            v *= static_cast<double>(scale);
-            ids[lane] = isel;
-            wout[lane] = static_cast<float>(v);
-        } else {
-            ids[lane] = -1;
-            wout[lane] = 0.0f;
+    double v = wsel;
+    if (norm && k > 1) v /= d;
+    v *= static_cast<double>(scale);
+    return SelOut{isel, static_cast<float>(v), k};
+}
+
+// Fast top-k stage on 32-bit keys.  After the group stage (exact fp64, as in
+// select_reg), each candidate's choice score is rounded to fp32 and mapped to
+// a monotonic unsigned key; rounding to nearest is monotonic, so a strict key
+// order is the fp64 order.  Each pick is a wave max of keys (DPP max chain,
+// one instruction per step) and a ballot for the owner.  If any pick finds
+// two candidates with its key (an fp32-level tie, or equal -inf scores), the
+// function returns false and the caller runs the exact fp64 selection, so
+// the decisions are always those of select_reg.
+__device__ __forceinline__ uint32_t fkey(double c) {
+    const uint32_t b = __float_as_uint(static_cast<float>(c));
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+template <int CTRL, int RM>
+__device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v) {
+    const uint32_t o = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), CTRL, RM, 0xF, false));
+    return v > o ? v : o;
+}
+
+template <int EPL>
+__device__ __forceinline__ bool select_fast(const SelIn<EPL>& in, int n_experts, int n_group,
+                                            int topk_group, int top_k, int norm, float scale,
+                                            SelOut* out) {
+    const int lane = threadIdx.x & 63;
+    const SelState<EPL> st = sel_groups<EPL>(in, n_experts, n_group, topk_group);
+    const double* s = st.s;
+    const int nres = st.nres;
+    uint32_t key[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) key[i] = fkey(st.c[i]);
+    const int k = min(top_k, nres);
+    double wsum = 0.0, wsel = 0.0;
+    int isel = -1;
+    for (int r = 0; r < k; ++r) {
+        uint32_t m = key[0];
+#pragma unroll
+        for (int i = 1; i < EPL; ++i) m = key[i] > m ? key[i] : m;
+        m = dpp_max_u32<0x111, 0xF>(m);
+        m = dpp_max_u32<0x112, 0xF>(m);
+        m = dpp_max_u32<0x114, 0xF>(m);
+        m = dpp_max_u32<0x118, 0xF>(m);
+        m = dpp_max_u32<0x142, 0xA>(m);
+        m = dpp_max_u32<0x143, 0xC>(m);
+        const uint32_t M = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), 63));
+        int hits = 0, owner = -1, slot = 0;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+            const unsigned long long b = __ballot(key[i] == M);
+            hits += __popcll(b);
+            if (b != 0ull) {
+                owner = __builtin_ctzll(b);
+                slot = i;
+            }
         }
+        if (hits != 1) return false;  // key tie: exact path decides
+        const int bi = owner * EPL + slot;
+        double sv = 0.0;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i)
+            if (i == slot) sv = s[i];
+        sv = readlane_d(sv, owner);
+        if (lane == owner) {
+#pragma unroll
+            for (int i = 0; i < EPL; ++i)
+                if (i == slot) key[i] = 0u;  // taken: below every score key
+        }
+        if (lane == r) { isel = bi; wsel = sv; }
+        wsum += sv;
+    }
+    const double d = wsum + 1e-20;
+    double v = wsel;
+    if (norm && k > 1) v /= d;
+    v *= static_cast<double>(scale);
+    *out = SelOut{isel, static_cast<float>(v), k};
+    return true;
+}
+
+template <int EPL>
+__device__ __forceinline__ SelOut select_any_reg(const SelIn<EPL>& in, int n_experts, int n_group,
+                                                 int topk_group, int top_k, int norm, float scale) {
+    SelOut o;
+    if (!select_fast<EPL>(in, n_experts, n_group, topk_group, top_k, norm, scale, &o))
+        o = select_reg<EPL>(in, n_experts, n_group, topk_group, top_k, norm, scale);
+    return o;
+}
+
+__device__ __forceinline__ void write_sel(const SelOut& o, int top_k, int32_t* ids, float* wout) {
+    const int lane = threadIdx.x & 63;
+    if (lane < top_k) {
+        ids[lane] = lane < o.kk ? o.isel : -1;
+        wout[lane] = lane < o.kk ? o.w : 0.0f;
     }
 }
 
+template <int EPL>
+__device__ __forceinline__ void select_token_reg(const double* lrow, const float* bias, const uint8_t* resident,
+                                 int n_experts, int n_group, int topk_group, int top_k, int norm,
+                                 float scale, int32_t* ids, float* wout) {
+    SelIn<EPL> in;
+    sel_load<EPL>(in, lrow, bias, resident);
+    write_sel(select_any_reg<EPL>(in, n_experts, n_group, topk_group, top_k, norm, scale), top_k, ids,
+              wout);
+}
+
 // Dispatch on experts per lane; fallback = the LDS version.
-__device__ void select_any(const double* lrow, const float* bias, const uint8_t* resident,
+__device__ __forceinline__ void select_any(const double* lrow, const float* bias, const uint8_t* resident,
                            int n_experts, int n_group, int topk_group, int top_k, int norm,
                            float scale, int32_t* ids, float* wout, int epl, double* c, double* s,
                            uint8_t* gsel) {
@@ -401,12 +666,13 @@ __device__ __forceinline__ bool dup_route(const int32_t* ids, int i, int top_k) 
 }
 
 // ---------------------------------------------------------------------------
-// Planner (one workgroup, any blockDim multiple of 64).  Counting sort of the
-// (token, k) assignments by expert id; slots in ascending expert id, shared
-// expert last; items of <= item_cap pairs.  The order of pairs inside a slot
+// General planner (one workgroup, any blockDim multiple of 64).  Counting
+// sort of the (token, k) assignments by expert id; slots in ascending expert
+// id, shared expert last with pairs [0, T); routed pairs from T; items of
+// <= item_cap pairs, routed items first.  The order of pairs inside a slot
 // only picks an MFMA column, which never changes a value, so the atomic
 // cursor keeps the results deterministic.  LDS: 2*E + blockDim ints.
-__device__ int block_excl_scan(int v, int* tmp, int* total) {
+__device__ __forceinline__ int block_excl_scan(int v, int* tmp, int* total) {
     const int tid = threadIdx.x, n = blockDim.x;
     tmp[tid] = v;
     __syncthreads();
@@ -422,7 +688,7 @@ __device__ int block_excl_scan(int v, int* tmp, int* total) {
     return incl - v;
 }
 
-__device__ void plan_build(const int32_t* __restrict__ ids, const float* __restrict__ w,
+__device__ __forceinline__ void plan_build(const int32_t* __restrict__ ids, const float* __restrict__ w,
                            int n_tokens, int top_k, const cx_expert_desc* table, int n_experts,
                            int has_shared, int item_cap, int max_items, const PlanPtrs& P,
                            int* err_flag, int* sm /* 2E + blockDim */) {
@@ -444,6 +710,8 @@ __device__ void plan_build(const int32_t* __restrict__ ids, const float* __restr
         atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
+    const bool shared = has_shared && table[n_experts].w_up != nullptr;
+    const int s0 = shared ? n_tokens : 0;  // first routed pair
     const int chunk = (n_experts + nt - 1) / nt;
     const int e0 = min(tid * chunk, n_experts), e1 = min(e0 + chunk, n_experts);
     int my_pairs = 0, my_slots = 0;
@@ -452,7 +720,7 @@ __device__ void plan_build(const int32_t* __restrict__ ids, const float* __restr
         my_slots += cnt[e] > 0;
     }
     int tot_pairs = 0, tot_slots = 0;
-    int pair_off = block_excl_scan(my_pairs, scan, &tot_pairs);
+    int pair_off = s0 + block_excl_scan(my_pairs, scan, &tot_pairs);
     int slot_off = block_excl_scan(my_slots, scan, &tot_slots);
     for (int e = e0; e < e1; ++e) {
         cur[e] = pair_off;
@@ -476,30 +744,27 @@ __device__ void plan_build(const int32_t* __restrict__ ids, const float* __restr
         }
         P.token_pairs[(size_t)t * (top_k + 1) + k] = pos;
     }
-    const bool shared = has_shared && table[n_experts].w_up != nullptr;
     for (int t = tid; t < n_tokens; t += nt) {
-        int pos = -1;
         if (shared) {
-            pos = tot_pairs + t;
-            P.pair_token[pos] = t;
-            P.pair_weight[pos] = 1.0f;
+            P.pair_token[t] = t;
+            P.pair_weight[t] = 1.0f;
         }
-        P.token_pairs[(size_t)t * (top_k + 1) + top_k] = pos;
+        P.token_pairs[(size_t)t * (top_k + 1) + top_k] = shared ? t : -1;
     }
     if (shared && tid == 0) {
         P.slot_expert[tot_slots] = n_experts;
-        P.slot_pair_begin[tot_slots] = tot_pairs;
+        P.slot_pair_begin[tot_slots] = 0;
         P.slot_pair_count[tot_slots] = n_tokens;
     }
     __syncthreads();
     const int n_slots = tot_slots + (shared ? 1 : 0);
     const int schunk = (n_slots + nt - 1) / nt;
-    const int s0 = min(tid * schunk, n_slots), s1 = min(s0 + schunk, n_slots);
+    const int s0s = min(tid * schunk, n_slots), s1s = min(s0s + schunk, n_slots);
     int my_items = 0;
-    for (int s = s0; s < s1; ++s) my_items += (P.slot_pair_count[s] + item_cap - 1) / item_cap;
+    for (int s = s0s; s < s1s; ++s) my_items += (P.slot_pair_count[s] + item_cap - 1) / item_cap;
     int tot_items = 0;
     int it = block_excl_scan(my_items, scan, &tot_items);
-    for (int s = s0; s < s1; ++s) {
+    for (int s = s0s; s < s1s; ++s) {
         const int pb = P.slot_pair_begin[s], pc = P.slot_pair_count[s];
         for (int o = 0; o < pc; o += item_cap) {
             if (it < max_items) {
@@ -518,176 +783,27 @@ __device__ void plan_build(const int32_t* __restrict__ ids, const float* __restr
     }
     for (int i = tid; i < min(tot_items, max_items); i += nt) {
         const cx_expert_desc& e = table[P.slot_expert[P.item_slot[i]]];
-        P.item_rec[i] = ItemRec{e.w_up, e.w_gate, e.w_down, e.s_up, e.s_gate, e.s_down,
-                                P.item_pair_begin[i], P.item_pair_count[i], e.up_rb, e.gate_rb,
-                                e.down_rb, 0};
-    }
-    // token-dense map for the decode down kernel: slot_tok_pair[s][t], t < 16
-    if (P.slot_tok_pair != nullptr && n_tokens <= kTileTok) {
-        __syncthreads();
-        for (int i = tid; i < n_slots * kTileTok; i += nt) P.slot_tok_pair[i] = -1;
-        __syncthreads();
-        for (int s = tid; s < n_slots; s += nt) {
-            const int pb = P.slot_pair_begin[s], pc = P.slot_pair_count[s];
-            for (int q = 0; q < pc; ++q) P.slot_tok_pair[s * kTileTok + P.pair_token[pb + q]] = pb + q;
-        }
+        const int pb = P.item_pair_begin[i], np = P.item_pair_count[i];
+        const int t0 = P.pair_token[pb];
+        const int t1 = np > 1 ? P.pair_token[pb + 1] : 0;
+        const int t2 = np > 2 ? P.pair_token[pb + 2] : 0;
+        const int t3 = np > 3 ? P.pair_token[pb + 3] : 0;
+        P.item_rec[i] = ItemRec{e.w_up, e.w_gate, e.w_down, e.s_up, e.s_gate, e.s_down, pb, np,
+                                e.up_rb, e.gate_rb, e.down_rb, 0, {t0, t1, t2, t3}};
     }
     if (tid == 0) {
+        const int shared_items = shared ? (n_tokens + item_cap - 1) / item_cap : 0;
         if (tot_items > max_items) s_err |= kErrPlanOverflow;
         P.hdr->n_slots = n_slots;
         P.hdr->n_items = min(tot_items, max_items);
-        P.hdr->n_pairs = tot_pairs + (shared ? n_tokens : 0);
+        P.hdr->n_pairs = s0 + tot_pairs;
+        P.hdr->n_routed_slots = tot_slots;
+        P.hdr->n_routed_items = min(tot_items - shared_items, max_items);
         if (s_err) atomicOr(err_flag, s_err);
     }
 }
 
-// Orders LDS traffic between lanes of one wave (compiler barrier; the LDS
-// itself executes a wave's instructions in order).
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-}
-
-// Planner for n_tokens <= 16 run by ONE wave, no barriers and no atomics on
-// global memory: same layout and order as plan_build (slots ascending by
-// expert id, shared expert last, one item per slot since a slot holds <= 16
-// pairs; pairs of a slot in assignment order).  Every output cell is written
-// exactly once.  LDS: 3*E + 3*n_tokens*top_k ints.
-__device__ void plan_wave(const int32_t* __restrict__ ids, const float* __restrict__ w,
-                          int n_tokens, int top_k, const cx_expert_desc* table, int n_experts,
-                          int has_shared, const PlanPtrs& P, int* err_flag, int* sm) {
-    const int lane = threadIdx.x & 63;
-    const int n_assign = n_tokens * top_k;
-    int* cnt = sm;                      // [E] kept pairs per expert
-    int* first = sm + n_experts;        // [E] first pair of the expert's slot
-    int* slot_of = sm + 2 * n_experts;  // [E] slot index (where cnt > 0)
-    int* eid = sm + 3 * n_experts;      // [n_assign] expert of a kept assignment, else -1
-    int* pos = eid + n_assign;          // [n_assign] pair index or -1
-    int err = 0;
-    for (int e = lane; e < n_experts; e += 64) cnt[e] = 0;
-    for (int i = lane; i < n_assign; i += 64) {
-        int e = ids[i];
-        if (e >= n_experts) { err |= kErrBadExpertId; e = -1; }
-        else if (e >= 0 && table[e].w_up == nullptr) { err |= kErrNotResident; e = -1; }
-        else if (e >= 0 && dup_route(ids, i, top_k)) { err |= kErrDuplicateRoute; e = -1; }
-        eid[i] = e < 0 ? -1 : e;
-    }
-    wave_sync();
-    for (int i = lane; i < n_assign; i += 64)
-        if (eid[i] >= 0) atomicAdd(&cnt[eid[i]], 1);
-    wave_sync();
-    const int chunk = (n_experts + 63) / 64;
-    const int e0 = min(lane * chunk, n_experts), e1 = min(e0 + chunk, n_experts);
-    int mp = 0, ms = 0;
-    for (int e = e0; e < e1; ++e) { mp += cnt[e]; ms += cnt[e] > 0; }
-    int ip = mp, is = ms;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int a = __shfl_up(ip, off, 64), b = __shfl_up(is, off, 64);
-        if (lane >= off) { ip += a; is += b; }
-    }
-    const int tot_pairs = __shfl(ip, 63, 64), tot_slots = __shfl(is, 63, 64);
-    int po = ip - mp, so = is - ms;
-    for (int e = e0; e < e1; ++e) {
-        const int n = cnt[e];
-        first[e] = po;
-        slot_of[e] = so;
-        if (n > 0) {
-            const cx_expert_desc& d = table[e];
-            P.slot_expert[so] = e;
-            P.slot_pair_begin[so] = po;
-            P.slot_pair_count[so] = n;
-            P.slot_rec[so] = SlotRec{d.w_down, d.s_down, d.down_rb, 0};
-            P.item_slot[so] = so;
-            P.item_pair_begin[so] = po;
-            P.item_pair_count[so] = n;
-            P.item_rec[so] = ItemRec{d.w_up, d.w_gate, d.w_down, d.s_up, d.s_gate, d.s_down, po, n,
-                                     d.up_rb, d.gate_rb, d.down_rb, 0};
-            ++so;
-        }
-        po += n;
-    }
-    wave_sync();
-    // pair position = first pair of the slot + earlier kept assignments of e
-    for (int i = lane; i < n_assign; i += 64) {
-        const int e = eid[i];
-        const int t = i / top_k, k = i - t * top_k;
-        int q = -1;
-        if (e >= 0) {
-            int before = 0;
-            for (int j = 0; j < i; ++j) before += eid[j] == e;
-            q = first[e] + before;
-            P.pair_token[q] = t;
-            P.pair_weight[q] = w[i];
-        }
-        pos[i] = q;
-        P.token_pairs[(size_t)t * (top_k + 1) + k] = q;
-    }
-    wave_sync();
-    // token-dense map: cell (s, t) = pair of token t in slot s, or -1
-    for (int cell = lane; cell < tot_slots * kTileTok; cell += 64) {
-        const int sl = cell / kTileTok, t = cell - sl * kTileTok;
-        int q = -1;
-        if (t < n_tokens) {
-            for (int k = 0; k < top_k; ++k) {
-                const int i = t * top_k + k;
-                const int e = eid[i];
-                if (e >= 0 && slot_of[e] == sl) q = pos[i];
-            }
-        }
-        P.slot_tok_pair[cell] = q;
-    }
-    const bool shared = has_shared && table[n_experts].w_up != nullptr;
-    const int n_slots = tot_slots + (shared ? 1 : 0);
-    if (shared) {
-        const cx_expert_desc& d = table[n_experts];
-        if (lane == 0) {
-            P.slot_expert[tot_slots] = n_experts;
-            P.slot_pair_begin[tot_slots] = tot_pairs;
-            P.slot_pair_count[tot_slots] = n_tokens;
-            P.slot_rec[tot_slots] = SlotRec{d.w_down, d.s_down, d.down_rb, 0};
-            P.item_slot[tot_slots] = tot_slots;
-            P.item_pair_begin[tot_slots] = tot_pairs;
-            P.item_pair_count[tot_slots] = n_tokens;
-            P.item_rec[tot_slots] = ItemRec{d.w_up, d.w_gate, d.w_down, d.s_up, d.s_gate, d.s_down,
-                                            tot_pairs, n_tokens, d.up_rb, d.gate_rb, d.down_rb, 0};
-        }
-        for (int t = lane; t < kTileTok; t += 64) {
-            const int q = tot_pairs + t;
-            if (t < n_tokens) {
-                P.pair_token[q] = t;
-                P.pair_weight[q] = 1.0f;
-                P.token_pairs[(size_t)t * (top_k + 1) + top_k] = q;
-            }
-            P.slot_tok_pair[tot_slots * kTileTok + t] = t < n_tokens ? q : -1;
-        }
-    } else {
-        for (int t = lane; t < n_tokens; t += 64) P.token_pairs[(size_t)t * (top_k + 1) + top_k] = -1;
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) err |= __shfl_xor(err, off, 64);
-    if (lane == 0) {
-        P.hdr->n_slots = n_slots;
-        P.hdr->n_items = n_slots;
-        P.hdr->n_pairs = tot_pairs + (shared ? n_tokens : 0);
-        if (err) atomicOr(err_flag, err);
-    }
-}
-
-size_t plan_wave_lds(int n_experts, int n_tokens, int top_k) {
-    return sizeof(int) * (3 * (size_t)n_experts + 2 * (size_t)n_tokens * top_k);
-}
-
 constexpr int kPlanThreads = 1024;
-
-__global__ __launch_bounds__(64) void k_plan_wave(const int32_t* __restrict__ ids,
-                                                  const float* __restrict__ w, int n_tokens,
-                                                  int top_k, const cx_expert_desc* table,
-                                                  int n_experts, int has_shared, PlanPtrs P,
-                                                  int* err_flag) {
-    extern __shared__ int smw[];
-    plan_wave(ids, w, n_tokens, top_k, table, n_experts, has_shared, P, err_flag, smw);
-}
 
 __global__ __launch_bounds__(kPlanThreads) void k_plan(const int32_t* __restrict__ ids,
                                                        const float* __restrict__ w, int n_tokens,
@@ -697,6 +813,151 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(const int32_t* __restrict
     extern __shared__ int sm[];
     plan_build(ids, w, n_tokens, top_k, table, n_experts, has_shared, item_cap, max_items, P,
                err_flag, sm);
+}
+
+// ---------------------------------------------------------------------------
+// Decode planner (T <= 16 tokens, E <= 256 experts, one thread per expert).
+// Input: the token x expert selection in LDS (bit e of mask[t] set when
+// token t routes to expert e, with its weight wsel[t][e] and top-k position
+// ksel[t][e]) and a copy of the layer table.  Output: the same plan layout
+// as plan_build, deterministic by construction (no atomics on the order):
+// slots in ascending expert id, a slot's pairs in ascending token order
+// starting at T (pairs [0, T) are the shared expert's), one item per slot,
+// the shared expert's slot and item last, and each pair's y_part row
+// (pair_row: t for the shared expert, T + t*K + k for route k of token t).
+// Every output cell is written exactly once, and every global input was
+// fetched before the selection, so the planner itself only waits on LDS.
+struct DecPlanLds {
+    cx_expert_desc tab[kDecMaxExperts + 1];
+    uint32_t mask[kTileTok][kDecMaxExperts / 32];
+    float wsel[kTileTok][kDecMaxExperts];
+    uint8_t ksel[kTileTok][kDecMaxExperts];
+    int scan[16][2];
+    int err;
+    int nres_w[16];  // resident experts counted per wave (selection of the decode stage)
+};
+
+// Copies table entries [0, E] (entry E = shared expert, zeroed when absent)
+// into LDS and clears the selection mask.
+__device__ __forceinline__ void dec_plan_prologue(DecPlanLds& S, const cx_expert_desc* table,
+                                                  int n_experts) {
+    constexpr int kChunks = sizeof(cx_expert_desc) / 16;
+    static_assert(sizeof(cx_expert_desc) % 16 == 0, "descriptor is copied in 16-byte chunks");
+    const int n = (n_experts + 1) * kChunks;
+    const u32x4* src = reinterpret_cast<const u32x4*>(table);
+    u32x4* dst = reinterpret_cast<u32x4*>(S.tab);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) dst[i] = ld16(src + i);
+    uint32_t* m = &S.mask[0][0];
+    for (int i = threadIdx.x; i < kTileTok * (kDecMaxExperts / 32); i += blockDim.x) m[i] = 0u;
+    if (threadIdx.x == 0) S.err = 0;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave by DPP row shifts and row
+// broadcasts (no LDS round trips).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x111, 0xF, 0xF, false));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x112, 0xF, 0xF, false));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x114, 0xF, 0xF, false));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x118, 0xF, 0xF, false));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x142, 0xA, 0xF, false));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x143, 0xC, 0xF, false));
+    return v;
+}
+
+__device__ __forceinline__ void dec_plan_core(DecPlanLds& S, int T, int K, int E, int has_shared,
+                                              const PlanPtrs& P, int* err_flag, int err) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int e = tid;
+    int cnt = 0;
+    if (e < E) {
+        for (int t = 0; t < T; ++t) cnt += (S.mask[t][e >> 5] >> (e & 31)) & 1u;
+        if (cnt > 0 && S.tab[e].w_up == nullptr) {  // routed to an expert the layer lacks
+            err |= kErrNotResident;
+            for (int t = 0; t < T; ++t)
+                if ((S.mask[t][e >> 5] >> (e & 31)) & 1u)
+                    P.token_pairs[(size_t)t * (K + 1) + S.ksel[t][e]] = -1;
+            cnt = 0;
+        }
+    }
+    // block-wide exclusive scan of (pairs, slots) in expert order, packed as
+    // pairs | slots << 16 (pairs <= 16 * 64, slots <= 256)
+    const uint32_t mine = static_cast<uint32_t>(cnt) | (cnt > 0 ? 0x10000u : 0u);
+    const uint32_t incl = wave_incl_scan(mine);
+    if (lane == 63) S.scan[wave][0] = static_cast<int>(incl);
+    __syncthreads();
+    uint32_t before = 0, total = 0;
+    for (int w = 0; w < nw; ++w) {
+        const uint32_t v = static_cast<uint32_t>(S.scan[w][0]);
+        before += w < wave ? v : 0u;
+        total += v;
+    }
+    const uint32_t excl = before + incl - mine;
+    const int tp = static_cast<int>(total & 0xFFFFu), ts = static_cast<int>(total >> 16);
+    const bool shared = has_shared && S.tab[E].w_up != nullptr;
+    const int s0 = shared ? T : 0;
+    if (cnt > 0) {
+        const int first = s0 + static_cast<int>(excl & 0xFFFFu);
+        const int slot = static_cast<int>(excl >> 16);
+        const cx_expert_desc d = S.tab[e];
+        P.slot_expert[slot] = e;
+        P.slot_pair_begin[slot] = first;
+        P.slot_pair_count[slot] = cnt;
+        P.slot_rec[slot] = SlotRec{d.w_down, d.s_down, d.down_rb, 0};
+        P.item_slot[slot] = slot;
+        P.item_pair_begin[slot] = first;
+        P.item_pair_count[slot] = cnt;
+        int tk0 = 0, tk1 = 0, tk2 = 0, tk3 = 0;  // first 4 tokens (registers, not a
+        int j = 0;                                // dynamically indexed array)
+        for (int t = 0; t < T; ++t) {
+            if ((S.mask[t][e >> 5] >> (e & 31)) & 1u) {
+                tk0 = j == 0 ? t : tk0;
+                tk1 = j == 1 ? t : tk1;
+                tk2 = j == 2 ? t : tk2;
+                tk3 = j == 3 ? t : tk3;
+                const int q = first + j++;
+                const int k = S.ksel[t][e];
+                P.pair_token[q] = t;
+                P.pair_weight[q] = S.wsel[t][e];
+                P.pair_row[q] = s0 + t * K + k;
+                P.token_pairs[(size_t)t * (K + 1) + k] = q;
+            }
+        }
+        P.item_rec[slot] = ItemRec{d.w_up, d.w_gate, d.w_down, d.s_up, d.s_gate, d.s_down, first, cnt,
+                                   d.up_rb, d.gate_rb, d.down_rb, 0, {tk0, tk1, tk2, tk3}};
+    }
+    if (shared) {
+        if (tid == 0) {
+            const cx_expert_desc d = S.tab[E];
+            P.slot_expert[ts] = E;
+            P.slot_pair_begin[ts] = 0;
+            P.slot_pair_count[ts] = T;
+            P.slot_rec[ts] = SlotRec{d.w_down, d.s_down, d.down_rb, 0};
+            P.item_slot[ts] = ts;
+            P.item_pair_begin[ts] = 0;
+            P.item_pair_count[ts] = T;
+            P.item_rec[ts] = ItemRec{d.w_up, d.w_gate, d.w_down, d.s_up, d.s_gate, d.s_down, 0, T,
+                                     d.up_rb, d.gate_rb, d.down_rb, 0, {0, 1, 2, 3}};
+        }
+        if (tid < T) {
+            P.pair_token[tid] = tid;
+            P.pair_weight[tid] = 1.0f;
+            P.pair_row[tid] = tid;
+            P.token_pairs[(size_t)tid * (K + 1) + K] = tid;
+        }
+    } else if (tid < T) {
+        P.token_pairs[(size_t)tid * (K + 1) + K] = -1;
+    }
+    if (err) atomicOr(&S.err, err);
+    __syncthreads();
+    if (tid == 0) {
+        const int ns = ts + (shared ? 1 : 0);
+        P.hdr->n_slots = ns;
+        P.hdr->n_items = ns;
+        P.hdr->n_pairs = s0 + tp;
+        P.hdr->n_routed_slots = ts;
+        P.hdr->n_routed_items = ts;
+        if (S.err) atomicOr(err_flag, S.err);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -713,21 +974,54 @@ struct FusedArgs {
     int32_t* ids;
     float* wout;
     int epl;               // experts per lane of the register selection, 0 = LDS fallback
-    // optional planner
-    int do_plan;
+    // planner
     const cx_expert_desc* table;
     int has_shared, item_cap, max_items;
     PlanPtrs plan;
     int* err_flag;
 };
 
-// T <= 16: selection of every token (wave t selects token t; with the
-// register path all tokens run in parallel) and, for cx_moe_layer, the
-// planner (one wave), in one workgroup after k_route_logits.  (A "last
-// workgroup" fusion into the logits kernel needs a device-scope fence per
-// workgroup, which on this multi-XCD part writes back L2 and costs far more
-// than the kernel boundary.)
-__global__ __launch_bounds__(1024) void k_route_select_plan(FusedArgs A) {
+FusedArgs fused_args(const RouteArgs& R) {
+    FusedArgs A{};
+    A.x = R.x;
+    A.x_dtype = R.x_dtype;
+    A.w = R.w;
+    A.w_dtype = R.w_dtype;
+    A.bias = R.bias;
+    A.resident = R.resident;
+    A.n_tokens = R.n_tokens;
+    A.hidden = R.hidden;
+    A.n_experts = R.n_experts;
+    A.n_group = R.n_group;
+    A.topk_group = R.topk_group;
+    A.top_k = R.top_k;
+    A.norm = R.norm;
+    A.scale = R.scale;
+    A.logits = R.logits;
+    A.ids = R.ids;
+    A.wout = R.wout;
+    if (R.plan != nullptr) {
+        A.table = R.table;
+        A.has_shared = R.has_shared;
+        A.item_cap = R.item_cap;
+        A.max_items = R.max_items;
+        A.plan = *R.plan;
+        A.err_flag = R.err_flag;
+    }
+    return A;
+}
+
+template <bool XF32, bool WF32>
+__global__ __launch_bounds__(kRouteThreads) void k_route_logits(FusedArgs A) {
+    __shared__ double red[4 * kRouteTB];
+    const int t0 = blockIdx.y * kRouteTB;
+    row_logits<XF32, WF32>(A.x, A.w, t0, min(kRouteTB, A.n_tokens - t0), A.hidden, A.n_experts,
+                           A.logits, red);
+}
+
+// T <= 16, selection only: wave t selects token t (register path: all tokens
+// in parallel; LDS fallback: 4 waves loop over the tokens).
+__global__ __launch_bounds__(1024) void k_route_select_small(FusedArgs A) {
     extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
     const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     double* c = reinterpret_cast<double*>(dyn) + (size_t)wave * 2 * A.n_experts;
@@ -738,21 +1032,6 @@ __global__ __launch_bounds__(1024) void k_route_select_plan(FusedArgs A) {
                    A.topk_group, A.top_k, A.norm, A.scale, A.ids + (size_t)t * A.top_k,
                    A.wout + (size_t)t * A.top_k, A.epl, c, s, gsel);
     }
-    if (A.do_plan) {
-        __threadfence_block();
-        __syncthreads();
-        if (wave == 0)
-            plan_wave(A.ids, A.wout, A.n_tokens, A.top_k, A.table, A.n_experts, A.has_shared,
-                      A.plan, A.err_flag, reinterpret_cast<int*>(dyn));
-    }
-}
-
-template <bool XF32, bool WF32>
-__global__ __launch_bounds__(kRouteThreads) void k_route_logits(FusedArgs A) {
-    __shared__ double red[4 * kRouteTB];
-    const int t0 = blockIdx.y * kRouteTB;
-    row_logits<XF32, WF32>(A.x, A.w, t0, min(kRouteTB, A.n_tokens - t0), A.hidden, A.n_experts,
-                           A.logits, red);
 }
 
 // one wave per token, 4 tokens per workgroup
@@ -767,6 +1046,157 @@ __global__ __launch_bounds__(kRouteThreads) void k_route_select(FusedArgs A) {
     select_any(A.logits + (size_t)t * A.n_experts, A.bias, A.resident, A.n_experts, A.n_group,
                A.topk_group, A.top_k, A.norm, A.scale, A.ids + (size_t)t * A.top_k,
                A.wout + (size_t)t * A.top_k, A.epl, c, s, gsel);
+}
+
+// ---------------------------------------------------------------------------
+// Decode stage 1: router logits, block b = expert row b % E for tokens
+// [4*(b/E), +4) (T <= 16).
+template <bool WF32>
+__global__ __launch_bounds__(kRouteThreads) void k_dec_logits(FusedArgs A) {
+    __shared__ double red[4 * 4];
+    const int e = blockIdx.x % A.n_experts, t0 = (blockIdx.x / A.n_experts) * 4;
+    row_logits4<WF32, kRouteThreads>(A.x, A.w, e, t0, min(4, A.n_tokens - t0), A.hidden,
+                                     A.n_experts, A.logits, red);
+}
+
+// Decode stage 2: workgroup 0 selects every token (wave t = token t,
+// register path) and builds the plan; blocks 1.. run the shared expert's
+// gate/up tiles (single mode, pairs [0, T)): KSA of the 16 waves split K, so
+// the whole expert is in flight while the latency-bound selection runs.
+// Every global input of workgroup 0 (logits, bias, resident mask, layer
+// table) is requested before its first barrier.  LDS (dynamic) is shared by
+// the two roles: the planner's DecPlanLds or the gate/up tile's reduction
+// tile and staged activations.
+template <int EPL, int NKB, int KSA, bool XLDS>
+__global__ __launch_bounds__(kDecThreads) void k_dec_select_sgu(FusedArgs A, ExpertLaunch SG) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char dlds[];
+    if (blockIdx.x > 0) {
+        // activations streamed from L2 ride the ring too: keep it 2 deep so
+        // the 16-wave block stays within 128 registers
+        constexpr int D = NKB < (XLDS ? 4 : 2) ? NKB : (XLDS ? 4 : 2);
+        gate_up_tile<NKB, D, 1, false, XLDS, kDecThreads / 64, true, KSA>(SG, blockIdx.x - 1, 0, dlds);
+        return;
+    }
+    DecPlanLds& S = *reinterpret_cast<DecPlanLds*>(dlds);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int T = A.n_tokens, K = A.top_k, E = A.n_experts, TE = T * E;
+    double* sS = reinterpret_cast<double*>(dlds + sizeof(DecPlanLds));  // [T][E]
+    double* sC = sS + TE;                                               // [T][E]
+    // 1) every global input at once: this thread's logits, bias and
+    //    residency (<= 4 (token, expert) cells), the layer table
+    constexpr int kCells = kTileTok * kDecMaxExperts / kDecThreads;
+    double lg[kCells];
+    float bs[kCells];
+    bool rs[kCells];
+#pragma unroll
+    for (int r = 0; r < kCells; ++r) {
+        const int i = tid + r * kDecThreads, e = i % E;
+        if (i < TE) {
+            lg[r] = A.logits[i];
+            bs[r] = A.bias[e];
+            rs[r] = A.resident == nullptr || A.resident[e] != 0;
+        }
+    }
+    dec_plan_prologue(S, A.table, E);
+    // 2) scores of every (token, expert) cell, spread over all 16 waves
+    int nres_part = 0;
+#pragma unroll
+    for (int r = 0; r < kCells; ++r) {
+        const int i = tid + r * kDecThreads;
+        if (i < TE) {
+            expert_scores(lg[r], bs[r], rs[r], &sS[i], &sC[i]);
+            nres_part += i < E && rs[r] ? 1 : 0;  // token 0's row counts each expert once
+        }
+    }
+    const uint32_t nres_wave = wave_incl_scan(static_cast<uint32_t>(nres_part));
+    if (lane == 63) S.nres_w[wave] = static_cast<int>(nres_wave);
+    __syncthreads();
+    // 3) selection: wave t = token t
+    if (wave < T) {
+        int nres = 0;
+#pragma unroll
+        for (int w = 0; w < kDecThreads / 64; ++w) nres += S.nres_w[w];
+        SelIn<EPL> in;
+        sel_load_lds<EPL>(in, sS + (size_t)wave * E, sC + (size_t)wave * E, nres);
+        const SelOut o = select_any_reg<EPL>(in, E, A.n_group, A.topk_group, K, A.norm, A.scale);
+        write_sel(o, K, A.ids + (size_t)wave * K, A.wout + (size_t)wave * K);
+        if (lane < o.kk) {
+            atomicOr(&S.mask[wave][o.isel >> 5], 1u << (o.isel & 31));
+            S.wsel[wave][o.isel] = o.w;
+            S.ksel[wave][o.isel] = static_cast<uint8_t>(lane);
+        } else if (lane < K) {
+            A.plan.token_pairs[(size_t)wave * (K + 1) + lane] = -1;
+        }
+    }
+    __syncthreads();
+    dec_plan_core(S, T, K, E, A.has_shared, A.plan, A.err_flag, 0);
+}
+
+// Decode stage 1' (routes given): workgroup 0 validates the routes (range,
+// repeats within a token: validate_routes, server/moe_layer_runtime.py:84-98)
+// and builds the plan; blocks 1.. run the shared expert's gate/up tiles.
+struct DecIdsArgs {
+    const int32_t* ids;
+    const float* w;
+    int n_tokens, top_k, n_experts, has_shared;
+    const cx_expert_desc* table;
+    PlanPtrs plan;
+    int* err_flag;
+};
+
+constexpr int kDecIdsPerThread = 4;  // T*K <= 16*64 assignments over 256 threads
+
+template <int NKB, bool F16>
+__global__ __launch_bounds__(kRouteThreads) void k_dec_plan_sgu(DecIdsArgs P, ExpertLaunch SG) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char dlds[];
+    if (blockIdx.x > 0) {
+        constexpr int D = NKB < 4 ? NKB : 4;
+        gate_up_tile<NKB, D, 1, F16, false, 4, true>(SG, blockIdx.x - 1, 0, dlds);
+        return;
+    }
+    DecPlanLds& S = *reinterpret_cast<DecPlanLds*>(dlds);
+    int* rid = reinterpret_cast<int*>(dlds + sizeof(DecPlanLds));  // [16 * 64]
+    const int tid = threadIdx.x;
+    const int T = P.n_tokens, K = P.top_k, E = P.n_experts, n = T * K;
+    int myid[kDecIdsPerThread];
+    float myw[kDecIdsPerThread];
+#pragma unroll
+    for (int r = 0; r < kDecIdsPerThread; ++r) {
+        const int i = tid + r * kRouteThreads;
+        myid[r] = i < n ? P.ids[i] : -1;
+        myw[r] = i < n ? P.w[i] : 0.0f;
+    }
+    dec_plan_prologue(S, P.table, E);
+#pragma unroll
+    for (int r = 0; r < kDecIdsPerThread; ++r) {
+        const int i = tid + r * kRouteThreads;
+        if (i < n) rid[i] = myid[r];
+    }
+    __syncthreads();
+    int err = 0;
+#pragma unroll
+    for (int r = 0; r < kDecIdsPerThread; ++r) {
+        const int i = tid + r * kRouteThreads;
+        if (i >= n) continue;
+        const int t = i / K, k = i - t * K, e = myid[r];
+        bool ok = e >= 0;
+        if (e >= E) {
+            err |= kErrBadExpertId;
+            ok = false;
+        } else if (ok) {
+            for (int j = t * K; j < i; ++j)
+                if (rid[j] == e) { err |= kErrDuplicateRoute; ok = false; break; }
+        }
+        if (ok) {
+            atomicOr(&S.mask[t][e >> 5], 1u << (e & 31));
+            S.wsel[t][e] = myw[r];
+            S.ksel[t][e] = static_cast<uint8_t>(k);
+        } else {
+            P.plan.token_pairs[(size_t)t * (K + 1) + k] = -1;
+        }
+    }
+    __syncthreads();
+    dec_plan_core(S, T, K, E, P.has_shared, P.plan, P.err_flag, err);
 }
 
 // Experts per lane for the register selection (E = 64*EPL, groups made of a
@@ -787,36 +1217,109 @@ size_t select_lds(int n_experts) {
     return (size_t)8 * n_experts * sizeof(double) + 4 * 64;
 }
 
+// Shared-expert gate/up tiling of stage 2 (16-wave blocks): k-blocks per
+// active wave (NKB) and active waves (KSA) for hidden / 128 k-blocks.
+template <int EPL, int XLDS>
+void go_dec_select_h(const FusedArgs& A, const ExpertLaunch* sg, size_t lds, hipStream_t s) {
+    ExpertLaunch none{};
+    const ExpertLaunch& G = sg ? *sg : none;
+    const dim3 grid(1 + (sg ? G.inter / kTileRows : 0)), block(kDecThreads);
+    switch (A.hidden / kKB) {
+        case 56: cx_launch((k_dec_select_sgu<EPL, 4, 14, XLDS>), grid, block, lds, s, A, G); break;
+        case 8: cx_launch((k_dec_select_sgu<EPL, 1, 8, XLDS>), grid, block, lds, s, A, G); break;
+        default: cx_launch((k_dec_select_sgu<EPL, 1, 4, XLDS>), grid, block, lds, s, A, G); break;
+    }
+}
+
+int dec_select_ksa(int hidden) {
+    switch (hidden / kKB) {
+        case 56: return 14;
+        case 8: return 8;
+        default: return 4;
+    }
+}
+
+template <int EPL>
+void go_dec_select(const FusedArgs& A, const ExpertLaunch* sg, hipStream_t s) {
+    const bool xl = sg != nullptr && sg->np_lds > 0;
+    size_t lds = sizeof(DecPlanLds) + (size_t)2 * A.n_tokens * A.n_experts * sizeof(double);
+    if (sg != nullptr)
+        lds = std::max(lds, gate_up_lds_bytes(dec_select_ksa(A.hidden), 1, xl ? sg->np_lds : 0, A.hidden));
+    if (xl) go_dec_select_h<EPL, true>(A, sg, lds, s);
+    else go_dec_select_h<EPL, false>(A, sg, lds, s);
+}
+
+template <int NKB>
+void go_dec_plan(const DecIdsArgs& P, const ExpertLaunch* sg, hipStream_t s) {
+    ExpertLaunch none{};
+    const ExpertLaunch& G = sg ? *sg : none;
+    const int grid = 1 + (sg ? G.inter / kTileRows : 0);
+    size_t lds = sizeof(DecPlanLds) + sizeof(int) * kTileTok * 64;
+    if (sg != nullptr) lds = std::max(lds, gate_up_lds_bytes(4, 1, 0, G.hidden));
+    if (sg && G.in_dtype == CX_DTYPE_FP16)
+        cx_launch((k_dec_plan_sgu<NKB, true>), dim3(grid), dim3(kRouteThreads), lds, s, P, G);
+    else
+        cx_launch((k_dec_plan_sgu<NKB, false>), dim3(grid), dim3(kRouteThreads), lds, s, P, G);
+}
+
 }  // namespace
 
-hipError_t launch_route(const RouteArgs& R, hipStream_t s) {
-    FusedArgs A{};
-    A.x = R.x;
-    A.x_dtype = R.x_dtype;
-    A.w = R.w;
-    A.w_dtype = R.w_dtype;
-    A.bias = R.bias;
-    A.resident = R.resident;
-    A.n_tokens = R.n_tokens;
-    A.hidden = R.hidden;
-    A.n_experts = R.n_experts;
-    A.n_group = R.n_group;
-    A.topk_group = R.topk_group;
-    A.top_k = R.top_k;
-    A.norm = R.norm;
-    A.scale = R.scale;
-    A.logits = R.logits;
-    A.ids = R.ids;
-    A.wout = R.wout;
-    A.do_plan = R.plan != nullptr;
-    if (R.plan != nullptr) {
-        A.table = R.table;
-        A.has_shared = R.has_shared;
-        A.item_cap = R.item_cap;
-        A.max_items = R.max_items;
-        A.plan = *R.plan;
-        A.err_flag = R.err_flag;
+bool dec_route_ok(int n_experts, int n_group) {
+    const int epl = register_epl(n_experts, n_group);
+    return n_experts <= kDecMaxExperts && (epl == 1 || epl == 2 || epl == 4);
+}
+
+int dec_sgu_np_lds(int hidden, int n_tokens, int max_lds) {
+    if (hidden % 512 != 0 || n_tokens > 4) return 0;
+    const int red = (int)gate_up_red_bytes(dec_select_ksa(hidden), 1);
+    const int rows = (std::min(max_lds, 65536) - red) / (hidden * 2 + 16);
+    return n_tokens <= rows ? n_tokens : 0;
+}
+
+bool dec_shared_ok(int hidden, int inter) {
+    const int nkh = hidden / kKB;
+    if (hidden % kKB != 0 || (nkh != 56 && nkh != 8 && nkh != 4)) return false;
+    return (inter == 2048 || inter == 512) && hidden % 64 == 0;
+}
+
+hipError_t launch_dec_logits(const RouteArgs& R, hipStream_t s) {
+    if (R.n_tokens > kTileTok || R.x_dtype != CX_DTYPE_BF16) return hipErrorInvalidValue;
+    const FusedArgs A = fused_args(R);
+    const dim3 grid(R.n_experts * ((R.n_tokens + 3) / 4));
+    if (R.w_dtype == CX_DTYPE_F32) cx_launch(k_dec_logits<true>, grid, dim3(kRouteThreads), 0, s, A);
+    else cx_launch(k_dec_logits<false>, grid, dim3(kRouteThreads), 0, s, A);
+    return hipGetLastError();
+}
+
+hipError_t launch_dec_select_sgu(const RouteArgs& R, const ExpertLaunch* sg, hipStream_t s) {
+    if (R.plan == nullptr || R.n_tokens > kTileTok || !dec_route_ok(R.n_experts, R.n_group))
+        return hipErrorInvalidValue;
+    const FusedArgs A = fused_args(R);
+    switch (register_epl(R.n_experts, R.n_group)) {
+        case 1: go_dec_select<1>(A, sg, s); break;
+        case 2: go_dec_select<2>(A, sg, s); break;
+        default: go_dec_select<4>(A, sg, s); break;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_dec_plan_sgu(const int32_t* ids, const float* w, int n_tokens, int top_k,
+                               const cx_expert_desc* table, int n_experts, int has_shared,
+                               PlanPtrs plan, int* err_flag, const ExpertLaunch* sg,
+                               hipStream_t s) {
+    if (n_tokens > kTileTok || n_experts > kDecMaxExperts || top_k > 64) return hipErrorInvalidValue;
+    DecIdsArgs P{ids, w, n_tokens, top_k, n_experts, has_shared, table, plan, err_flag};
+    switch (sg ? sg->hidden / kKB : 4) {
+        case 56: go_dec_plan<14>(P, sg, s); break;
+        case 8: go_dec_plan<2>(P, sg, s); break;
+        case 4: go_dec_plan<1>(P, sg, s); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_route(const RouteArgs& R, hipStream_t s) {
+    FusedArgs A = fused_args(R);
     A.epl = register_epl(R.n_experts, R.n_group);
     const size_t sel = A.epl ? 0 : select_lds(R.n_experts);
     const dim3 lg(R.n_experts, (R.n_tokens + kRouteTB - 1) / kRouteTB);
@@ -830,13 +1333,11 @@ hipError_t launch_route(const RouteArgs& R, hipStream_t s) {
     if (R.n_tokens <= kRouteTB) {
         // register path: one wave per token, all in parallel; fallback: 4 waves
         const int threads = A.epl ? 64 * R.n_tokens : kRouteThreads;
-        size_t lds = A.epl ? 0 : (size_t)2 * (threads / 64) * R.n_experts * sizeof(double) + (threads / 64) * 64;
-        const size_t plan_lds = plan_wave_lds(R.n_experts, R.n_tokens, R.top_k);
-        if (A.do_plan && plan_lds > lds) lds = plan_lds;
-        cx_launch(k_route_select_plan, dim3(1), dim3(threads), lds, s, A);
-        return hipGetLastError();
+        const size_t lds = A.epl ? 0 : (size_t)2 * (threads / 64) * R.n_experts * sizeof(double) + (threads / 64) * 64;
+        cx_launch(k_route_select_small, dim3(1), dim3(threads), lds, s, A);
+    } else {
+        cx_launch(k_route_select, dim3((R.n_tokens + 3) / 4), dim3(kRouteThreads), sel, s, A);
     }
-    cx_launch(k_route_select, dim3((R.n_tokens + 3) / 4), dim3(kRouteThreads), sel, s, A);
     err = hipGetLastError();
     if (err != hipSuccess || R.plan == nullptr) return err;
     return launch_plan(R.ids, R.wout, R.n_tokens, R.top_k, R.table, R.n_experts, R.has_shared,
@@ -846,15 +1347,10 @@ hipError_t launch_route(const RouteArgs& R, hipStream_t s) {
 hipError_t launch_plan(const int32_t* ids, const float* w, int n_tokens, int top_k,
                        const cx_expert_desc* table, int n_experts, int has_shared, int item_cap,
                        int max_items, PlanPtrs plan, int* err_flag, hipStream_t s) {
-    if (n_tokens <= kTileTok && item_cap >= kTileTok && plan.slot_tok_pair != nullptr) {
-        cx_launch(k_plan_wave, dim3(1), dim3(64), plan_wave_lds(n_experts, n_tokens, top_k),
-                           s, ids, w, n_tokens, top_k, table, n_experts, has_shared, plan, err_flag);
-        return hipGetLastError();
-    }
     const int threads = n_tokens * top_k <= 512 ? 256 : kPlanThreads;
     const size_t lds = sizeof(int) * (2 * (size_t)n_experts + threads);
     cx_launch(k_plan, dim3(1), dim3(threads), lds, s, ids, w, n_tokens, top_k, table,
-                       n_experts, has_shared, item_cap, max_items, plan, err_flag);
+              n_experts, has_shared, item_cap, max_items, plan, err_flag);
     return hipGetLastError();
 }
 

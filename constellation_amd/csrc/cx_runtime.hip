@@ -220,6 +220,7 @@ struct cx_layer {
     int fast = 1;                      // every resident expert fits the grouped kernels
     int hidden = 0, inter = 0;
     cx_expert_desc* table = nullptr;   // device [n_experts + 1], entry n_experts = shared
+    cx_expert_desc shared_desc{};      // host copy of the shared expert (when has_shared)
 };
 
 namespace {
@@ -283,9 +284,9 @@ struct PlanSizes {
     int max_slots, max_pairs, max_items, item_cap, maxt;
 };
 
-PlanSizes plan_sizes(int n_tokens, int top_k, int n_experts, int has_shared, bool prefill) {
+PlanSizes plan_sizes(int n_tokens, int top_k, int n_experts, int has_shared) {
     PlanSizes z;
-    z.maxt = (!prefill && n_tokens <= kTileTok) || n_tokens <= kTileTok ? 1 : 4;
+    z.maxt = n_tokens <= kTileTok ? 1 : 4;
     z.item_cap = kTileTok * z.maxt;
     z.max_slots = std::min(n_tokens * top_k, n_experts) + has_shared;
     z.max_pairs = n_tokens * top_k + n_tokens * has_shared;
@@ -293,13 +294,14 @@ PlanSizes plan_sizes(int n_tokens, int top_k, int n_experts, int has_shared, boo
     return z;
 }
 
-int carve_plan(cx_ctx* ctx, const PlanSizes& z, int n_tokens, int top_k, hipStream_t s,
-               PlanPtrs* P) {
-    const bool dense = n_tokens <= kTileTok;
+// dense: a decode plan (dec_plan_core), which also fills pair_row; the
+// general planner leaves it out.
+int carve_plan(cx_ctx* ctx, const PlanSizes& z, int n_tokens, int top_k, bool dense,
+               hipStream_t s, PlanPtrs* P) {
     const size_t recs = sizeof(ItemRec) * (size_t)z.max_items + sizeof(SlotRec) * (size_t)z.max_slots;
-    const size_t ints = 4 + 3 * (size_t)z.max_slots + 3 * (size_t)z.max_items +
+    const size_t ints = kPlanHdrInts + 3 * (size_t)z.max_slots + 3 * (size_t)z.max_items +
                         2 * (size_t)z.max_pairs + (size_t)n_tokens * (top_k + 1) +
-                        (dense ? (size_t)z.max_slots * kTileTok : 0);
+                        (dense ? (size_t)z.max_pairs : 0);
     int rc = ensure(&ctx->plan_buf, recs + ints * 4 + 256, s);
     if (rc) return rc;
     char* raw = static_cast<char*>(ctx->plan_buf.p);
@@ -307,7 +309,7 @@ int carve_plan(cx_ctx* ctx, const PlanSizes& z, int n_tokens, int top_k, hipStre
     P->slot_rec = reinterpret_cast<SlotRec*>(raw + sizeof(ItemRec) * (size_t)z.max_items);
     int* base = reinterpret_cast<int*>(raw + recs);
     P->hdr = reinterpret_cast<PlanHdr*>(base);
-    int* q = base + 4;
+    int* q = base + kPlanHdrInts;
     P->slot_expert = q; q += z.max_slots;
     P->slot_pair_begin = q; q += z.max_slots;
     P->slot_pair_count = q; q += z.max_slots;
@@ -317,7 +319,7 @@ int carve_plan(cx_ctx* ctx, const PlanSizes& z, int n_tokens, int top_k, hipStre
     P->pair_token = q; q += z.max_pairs;
     P->pair_weight = reinterpret_cast<float*>(q); q += z.max_pairs;
     P->token_pairs = q; q += (size_t)n_tokens * (top_k + 1);
-    P->slot_tok_pair = dense ? q : nullptr;
+    P->pair_row = dense ? q : nullptr;
     return CX_OK;
 }
 
@@ -335,13 +337,110 @@ int check_desc(const cx_expert_desc* e) {
 // Activation rows of one work item that fit the LDS budget next to the
 // reduction tile (<= 16 KB); 0 when staging is not worth it or not possible.
 int lds_rows(const cx_ctx* ctx, int hidden, int max_pairs_per_item) {
+    if (hidden % 512 != 0) return 0;  // rows are copied in 1 KB wave chunks
     const int budget = std::min(ctx->max_lds, 65536) - 16384;
     const int rows = budget / (hidden * 2 + 16);
     return (max_pairs_per_item <= rows && max_pairs_per_item <= 4) ? max_pairs_per_item : 0;
 }
 
-// Routed-expert compute; when `route` is given, the router (and for T <= 16
-// the planner, in the same launch) runs first on the same stream.
+// The decode pipeline (T <= 16) serves this layer / router shape.
+bool dec_path_ok(const cx_layer* layer, int top_k, const RouteArgs* route) {
+    if (layer->n_experts > 256 || top_k > 64) return false;
+    if (!dec_shared_ok(layer->hidden, layer->inter)) return false;
+    return route == nullptr ||
+           (route->x_dtype == CX_DTYPE_BF16 && dec_route_ok(route->n_experts, route->n_group));
+}
+
+// Decode pipeline for T <= 16 tokens (plan, h and y_part buffers ready):
+//   router:  logits -> [select + plan | shared gate/up] -> routed gate/up
+//            -> down (routed + shared items) -> combine
+//   routes:  [plan | shared gate/up] -> routed gate/up
+//            -> down (routed + shared items) -> combine
+// The shared expert's gate/up streams beside the latency-bound selection
+// and planner; the routed gate/up grid holds exactly the routed items (one
+// resident round at 8 experts), and the down grid adds the shared item.  The
+// combine sums in the reference's order: route order, shared expert last.
+int moe_decode(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int n_tokens,
+               const int32_t* ids, const float* w, int top_k, void* y, int out_dtype,
+               float* y_f32, hipStream_t s, RouteArgs* route, const PlanSizes& z,
+               const PlanPtrs& P) {
+    const int T = n_tokens;
+    const int np_lds = lds_rows(ctx, layer->hidden, T);
+    ExpertLaunch SG{};
+    SG.table = nullptr;
+    SG.single = layer->shared_desc;
+    SG.n_tokens = T;
+    SG.hidden = layer->hidden;
+    SG.inter = layer->inter;
+    SG.maxt = 1;
+    SG.x = x;
+    SG.in_dtype = in_dtype;
+    SG.h_hi = static_cast<uint16_t*>(ctx->hhi.p);  // shared pairs [0, T)
+    SG.h_lo = static_cast<uint16_t*>(ctx->hlo.p);
+    SG.y_part = static_cast<float*>(ctx->ypart.p);
+    SG.np_lds = route != nullptr ? dec_sgu_np_lds(layer->hidden, T, ctx->max_lds) : 0;
+    const ExpertLaunch* sg = layer->has_shared ? &SG : nullptr;
+    const int routed_items = std::min(T * top_k, layer->n_experts);
+    if (route != nullptr) {
+        route->plan = &P;
+        route->table = layer->table;
+        route->has_shared = layer->has_shared;
+        route->item_cap = z.item_cap;
+        route->max_items = z.max_items;
+        route->err_flag = ctx->err_flag;
+        {
+            Span sp(ctx, "route", s);
+            CX_HIP(launch_dec_logits(*route, s));
+        }
+        {
+            Span sp(ctx, "plan", s);
+            CX_HIP(launch_dec_select_sgu(*route, sg, s));
+        }
+    } else {
+        Span sp(ctx, "plan", s);
+        CX_HIP(launch_dec_plan_sgu(ids, w, T, top_k, layer->table, layer->n_experts,
+                                   layer->has_shared, P, ctx->err_flag, sg, s));
+    }
+    ExpertLaunch L{};
+    L.table = layer->table;
+    L.plan = P;
+    L.max_items = routed_items;
+    L.n_tokens = T;
+    L.hidden = layer->hidden;
+    L.inter = layer->inter;
+    L.maxt = 1;
+    L.x = x;
+    L.in_dtype = in_dtype;
+    L.h_hi = static_cast<uint16_t*>(ctx->hhi.p);
+    L.h_lo = static_cast<uint16_t*>(ctx->hlo.p);
+    L.y_part = static_cast<float*>(ctx->ypart.p);
+    L.y = y;
+    L.y_f32 = y_f32;
+    L.out_dtype = out_dtype;
+    L.np_lds = np_lds;
+    L.skip_shared = 1;
+    if (L.max_items > 0) {
+        Span sp(ctx, "gate_up", s);
+        CX_HIP(launch_gate_up(L, s));
+    }
+    // down: the routed items and the shared expert's item (last)
+    L.skip_shared = 0;
+    L.max_items = routed_items + layer->has_shared;
+    if (L.max_items > 0) {
+        Span sp(ctx, "down", s);
+        CX_HIP(launch_down(L, s));
+    }
+    {
+        Span sp(ctx, "combine", s);
+        CX_HIP(launch_combine_dec(P, route != nullptr ? route->wout : w, L.y_part, T, top_k,
+                                  layer->has_shared, layer->hidden, y, out_dtype, y_f32, s));
+    }
+    return CX_OK;
+}
+
+// Routed-expert compute; when `route` is given, the router runs first on the
+// same stream.  T <= 16 takes the decode pipeline where the shapes allow it;
+// otherwise route -> plan -> grouped gate/up -> per-pair down -> combine.
 int moe_run(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int n_tokens,
             const int32_t* ids, const float* w, int top_k, void* y, int out_dtype, float* y_f32,
             hipStream_t s, bool prefill, RouteArgs* route) {
@@ -355,15 +454,19 @@ int moe_run(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int
                                      "row blocks multiple of 16)");
     int rc = set_device(ctx->device);
     if (rc) return rc;
-    const PlanSizes z = plan_sizes(n_tokens, top_k, layer->n_experts, layer->has_shared, prefill);
+    const bool dec = !prefill && n_tokens <= kTileTok && dec_path_ok(layer, top_k, route);
+    PlanSizes z = plan_sizes(n_tokens, top_k, layer->n_experts, layer->has_shared);
+    if (dec) z.max_items = z.max_slots;  // one item per slot (<= 16 pairs each)
     if (z.max_pairs == 0) return fail(CX_EINVAL, "nothing to compute");
     PlanPtrs P;
-    if ((rc = carve_plan(ctx, z, n_tokens, top_k, s, &P))) return rc;
+    if ((rc = carve_plan(ctx, z, n_tokens, top_k, dec, s, &P))) return rc;
     const size_t H = layer->hidden, I = layer->inter;
     if ((rc = ensure(&ctx->hhi, (size_t)z.max_pairs * I * 2, s))) return rc;
     if ((rc = ensure(&ctx->hlo, (size_t)z.max_pairs * I * 2, s))) return rc;
-    const bool fused = n_tokens <= kTileTok && down_fused_ok(layer->inter);
-    if (!fused && (rc = ensure(&ctx->ypart, (size_t)z.max_pairs * H * 4, s))) return rc;
+    if ((rc = ensure(&ctx->ypart, (size_t)z.max_pairs * H * 4, s))) return rc;
+    if (dec)
+        return moe_decode(ctx, layer, x, in_dtype, n_tokens, ids, w, top_k, y, out_dtype, y_f32,
+                          s, route, z, P);
     if (route != nullptr) {
         route->plan = &P;
         route->table = layer->table;
@@ -394,16 +497,10 @@ int moe_run(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int
     L.y = y;
     L.y_f32 = y_f32;
     L.out_dtype = out_dtype;
-    L.fold_weight = fused ? 1 : 0;
     L.np_lds = z.maxt == 1 ? lds_rows(ctx, layer->hidden, std::min(n_tokens, z.item_cap)) : 0;
     {
         Span sp(ctx, "gate_up", s);
         CX_HIP(launch_gate_up(L, s));
-    }
-    if (fused) {
-        Span sp(ctx, "down", s);
-        CX_HIP(launch_down_fused(L, z.max_slots, s));
-        return CX_OK;
     }
     {
         Span sp(ctx, "down", s);
@@ -754,6 +851,7 @@ int cx_layer_create(cx_ctx* ctx, int n_experts, const cx_expert_desc* const* exp
     if (!L) return fail(CX_ENOMEM, "out of host memory");
     L->n_experts = n_experts;
     L->has_shared = shared ? 1 : 0;
+    L->shared_desc = host[n_experts];
     L->fast = fast;
     L->hidden = H;
     L->inter = I;

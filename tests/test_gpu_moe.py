@@ -245,3 +245,100 @@ def test_moe_duplicate_route_is_dropped_and_reported(gpu, oracle, T, prefill):
         assert rel_l2(yf.cpu().numpy(), ref) < 1e-5
     finally:
         _free(layer, experts, sh)
+
+
+@pytest.mark.parametrize("T,E,shared,wdtype,mask", [
+    (1, 64, True, torch.bfloat16, False), (2, 64, True, torch.bfloat16, False),
+    (5, 128, True, torch.float32, False), (16, 64, True, torch.bfloat16, False),
+    (3, 256, False, torch.bfloat16, False), (4, 64, True, torch.bfloat16, True),
+    (16, 256, True, torch.bfloat16, True)])
+def test_moe_layer_decode_pipeline(gpu, oracle, T, E, shared, wdtype, mask):
+    """cx_moe_layer for T <= 16 and register-selectable expert counts: router
+    logits beside the shared expert's gate/up, selection + planner beside the
+    shared expert's down, routed gate/up, routed down + combine + shared."""
+    print(f"[moe] decode pipeline T={T} E={E} shared={shared} w={wdtype} mask={mask}", flush=True)
+    H, I = 1024, 512
+    layer, experts, sh, cpu, cpu_sh = _make_layer(gpu, oracle, E, H, I, seed=61 + T, shared=shared)
+    try:
+        x, w, bias = _router_inputs(gpu, 62 + T, T, E, H)
+        w = w.to(wdtype)
+        res = None
+        rdev = None
+        if mask:
+            res = np.zeros(E, np.uint8)
+            res[::3] = 1
+            rdev = torch.from_numpy(res).cuda()
+        y, yf, ids, wts = gpu.moe_layer(layer, x, w, bias, resident=rdev, n_group=8, topk_group=4,
+                                        top_k=8, want_f32=True)
+        gpu.sync()
+        for t, (oi, ow, margins, _) in enumerate(_oracle_route(oracle, x, w, bias, resident=res)):
+            if min(margins) <= 1e-12:
+                continue
+            k = len(oi)
+            assert ids[t].cpu().tolist()[:k] == oi.tolist(), t
+            assert np.allclose(wts[t].cpu().numpy()[:k], ow, rtol=1e-6, atol=0), t
+        ref = _oracle_moe(oracle, cpu, cpu_sh, x.float().cpu().numpy(), ids.cpu().numpy(),
+                          wts.cpu().numpy())
+        yf = yf.cpu().numpy()
+        assert rel_l2(yf, ref) < 1e-5, rel_l2(yf, ref)
+        assert np.abs(yf - ref).max() < 2e-2
+        assert np.array_equal(_bits(y), oracle.encode_act(yf, BF16, "rne"))
+    finally:
+        _free(layer, experts, sh)
+
+
+@pytest.mark.parametrize("T,dtype", [(1, torch.float16), (7, torch.bfloat16), (16, torch.float16)])
+def test_moe_decode_given_routes_with_shared(gpu, oracle, T, dtype):
+    """cx_moe_decode (routes given): planner beside the shared expert's gate/up,
+    then routed gate/up and the down + combine over every slot."""
+    print(f"[moe] decode given routes T={T} {dtype}", flush=True)
+    E, H, I = 48, 1024, 512
+    layer, experts, sh, cpu, cpu_sh = _make_layer(gpu, oracle, E, H, I, seed=71 + T)
+    try:
+        x = gpu.gen_normal(72 + T, 1, (T, H), 1.0, dtype)
+        rng = np.random.default_rng(T)
+        ids = np.stack([rng.choice(E, 6, replace=False) for _ in range(T)]).astype(np.int32)
+        ids[0, 5] = -1  # an empty slot
+        wts = rng.uniform(0.05, 1.0, ids.shape).astype(np.float32)
+        y, yf = gpu.moe(layer, x, torch.from_numpy(ids).cuda(), torch.from_numpy(wts).cuda(),
+                        want_f32=True)
+        gpu.sync()
+        ref = _oracle_moe(oracle, cpu, cpu_sh, x.float().cpu().numpy(), ids, wts)
+        yf = yf.cpu().numpy()
+        assert rel_l2(yf, ref) < 1e-5, rel_l2(yf, ref)
+        enc = FP16 if dtype == torch.float16 else BF16
+        assert np.array_equal(_bits(y), oracle.encode_act(yf, enc, "rne"))
+    finally:
+        _free(layer, experts, sh)
+
+
+@pytest.mark.parametrize("T", [1, 16])
+def test_full_size_moe_layer(gpu, oracle, T):
+    """The benchmark path at DeepSeek-V3 shapes: cx_moe_layer with 256 resident
+    experts + shared, H=7168, I=2048, bf16 router (config 1 / config 2)."""
+    print(f"[moe] full-size layer T={T}", flush=True)
+    E, H = 256, 7168
+    from constellation_amd.engine import Expert, Layer
+    experts = [Expert.generate(0, 81, 0x3000 + 4 * e) for e in range(E)]
+    sh = Expert.generate(0, 81, 0x3000 + 4 * E)
+    layer = Layer(gpu, experts, sh)
+    try:
+        x, w, bias = _router_inputs(gpu, 82 + T, T, E, H)
+        y, yf, ids, wts = gpu.moe_layer(layer, x, w, bias, n_group=8, topk_group=4, top_k=8,
+                                        routed_scaling_factor=2.5, want_f32=True)
+        gpu.sync()
+        idn, wn = ids.cpu().numpy(), wts.cpu().numpy()
+        for t, (oi, ow, margins, _) in enumerate(_oracle_route(oracle, x, w, bias)):
+            if min(margins) <= 1e-12:
+                continue
+            assert idn[t].tolist() == oi.tolist(), t
+        used = sorted(set(idn.ravel().tolist()) - {-1})
+        cpu = {e: oracle.gen_expert(81, 0x3000 + 4 * e) for e in used}
+        cpu_sh = oracle.gen_expert(81, 0x3000 + 4 * E)
+        ref = _oracle_moe(oracle, [cpu.get(e) for e in range(E)], cpu_sh,
+                          x.float().cpu().numpy(), idn, wn)
+        yf = yf.cpu().numpy()
+        assert rel_l2(yf, ref) < 1e-5 and np.abs(yf - ref).max() < 2e-2
+        assert np.array_equal(_bits(y), oracle.encode_act(yf, BF16, "rne"))
+    finally:
+        _free(layer, experts, sh)
