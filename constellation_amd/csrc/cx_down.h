@@ -49,15 +49,26 @@ __device__ __forceinline__ void load_h8g(const uint16_t* hi, const uint16_t* lo,
 // ring to one step):
 //  * XL (np <= 4): the rows go to LDS by direct global->LDS DMA before the
 //    weight prologue; the loop issues weight loads only;
-//  * otherwise h rides the ring: each stage holds its k-block's weights and
-//    h (hi, lo) together, issued D steps ahead.
+//  * otherwise (more pairs) h is loaded one step ahead in the order that
+//    keeps its wait independent of younger weight loads (2-deep ring).
 constexpr int kDownRowsPerWG = kTileRows * kWaves;  // 64
 constexpr int kDownLdsRows = 4;
 
 template <int NKB, int D, bool SINGLE, bool XL>
+__device__ __forceinline__ void down_item_path(const ExpertLaunch& L, const Unit& u, int tile);
+
+// Per item: h staged in LDS (D-deep weight ring) when the item has <= 4
+// pairs, else h rides a 2-deep ring; both in one launch (uniform branch).
+template <int NKB, int D, bool SINGLE>
 __device__ __forceinline__ void down_item_tile(const ExpertLaunch& L, int tile, int item) {
     Unit u;
     if (!resolve_unit<SINGLE>(L, item, kTileTok, &u)) return;
+    if (u.np <= kDownLdsRows) down_item_path<NKB, D, SINGLE, true>(L, u, tile);
+    else down_item_path<NKB, 2, SINGLE, false>(L, u, tile);
+}
+
+template <int NKB, int D, bool SINGLE, bool XL>
+__device__ __forceinline__ void down_item_path(const ExpertLaunch& L, const Unit& u, int tile) {
     const int H = u.e.hidden, I = u.e.inter;
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int g = lane >> 4, c = lane & 15;
@@ -85,14 +96,16 @@ __device__ __forceinline__ void down_item_tile(const ExpertLaunch& L, int tile, 
                                                           : L.plan.pair_row[u.pb + min(c, u.np - 1)];
     const uint16_t* gh = L.h_hi + (size_t)(u.pb + hrow) * I + g * 32;
     const uint16_t* gl = L.h_lo + (size_t)(u.pb + hrow) * I + g * 32;
-    // 1) ring prologue
+    // 1) ring prologue.  Without XL, h is loaded one step ahead, issued
+    //    after the weights of that step and before the weights D steps
+    //    ahead, so waiting for it never waits for younger weight loads.
     u32x4 wb[D][2];
-    u32x4 hr[XL ? 1 : D][8];
+    u32x4 hr[8];
 #pragma unroll
     for (int s = 0; s < D && s < NKB; ++s) {
         wb[s][0] = ld16(pd + s * kKB);
         wb[s][1] = ld16(pd + s * kKB + 16);
-        if (!XL) load_h8g(gh + s * kKB, gl + s * kKB, hr[s]);
+        if (!XL && s == 0) load_h8g(gh, gl, hr);
     }
     __builtin_amdgcn_sched_barrier(0);
     float scd[NKB];
@@ -117,16 +130,16 @@ __device__ __forceinline__ void down_item_tile(const ExpertLaunch& L, int tile, 
             }
             acc += scd[k] * down_step(wb[s], hb);
         } else {
-            acc += scd[k] * down_step(wb[s], hr[s]);
+            acc += scd[k] * down_step(wb[s], hr);
         }
         // one k-block's product tile live at a time
         __builtin_amdgcn_sched_barrier(0);
+        if (!XL && k + 1 < NKB) load_h8g(gh + (k + 1) * kKB, gl + (k + 1) * kKB, hr);
         if (k + D < NKB) {
             wb[s][0] = ld16(pd + (k + D) * kKB);
             wb[s][1] = ld16(pd + (k + D) * kKB + 16);
-            if (!XL) load_h8g(gh + (k + D) * kKB, gl + (k + D) * kKB, hr[s]);
-            __builtin_amdgcn_sched_barrier(0);
         }
+        __builtin_amdgcn_sched_barrier(0);
     }
     if (c < u.np) {
         const size_t p = (size_t)prow;

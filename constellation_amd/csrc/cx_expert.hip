@@ -446,9 +446,9 @@ __global__ __launch_bounds__(256) void k_down_t(ExpertLaunch L) {
 // ---------------------------------------------------------------------------
 // Down projection per work item of <= 16 pairs: down_item_tile (cx_down.h),
 // grid = (hidden/64, items).
-template <int NKB, int D, bool SINGLE, bool XL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XL ? 4 : 2))) void k_down_item(ExpertLaunch L) {
-    down_item_tile<NKB, D, SINGLE, XL>(L, blockIdx.x, blockIdx.y);
+template <int NKB, int D, bool SINGLE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_down_item(ExpertLaunch L) {
+    down_item_tile<NKB, D, SINGLE>(L, blockIdx.x, blockIdx.y);
 }
 
 // ---------------------------------------------------------------------------
@@ -644,20 +644,11 @@ bool pick_gate_up(const ExpertLaunch& L, dim3 grid, hipStream_t s) {
 // decode grid of 8 experts x 112 tiles is resident at once).
 constexpr int kDownXlDepth = 6;
 
-// XL (h staged in LDS) when every item holds <= 4 pairs: at most 4 tokens
-// (np_lds_down set by the caller), else h rides the weight ring.
 template <int NKB>
 void go_down_item(const ExpertLaunch& L, dim3 grid, hipStream_t s) {
-    const bool single = L.table == nullptr;
-    const bool xl = L.n_tokens <= kDownLdsRows;
-    const size_t lds = xl ? down_item_lds(L.inter) : 0;
-    if (xl) {
-        if (single) cx_launch((k_down_item<NKB, kDownXlDepth, true, true>), grid, dim3(256), lds, s, L);
-        else cx_launch((k_down_item<NKB, kDownXlDepth, false, true>), grid, dim3(256), lds, s, L);
-    } else {
-        if (single) cx_launch((k_down_item<NKB, 4, true, false>), grid, dim3(256), 0, s, L);
-        else cx_launch((k_down_item<NKB, 4, false, false>), grid, dim3(256), 0, s, L);
-    }
+    const size_t lds = down_item_lds(L.inter);
+    if (L.table == nullptr) cx_launch((k_down_item<NKB, kDownXlDepth, true>), grid, dim3(256), lds, s, L);
+    else cx_launch((k_down_item<NKB, kDownXlDepth, false>), grid, dim3(256), lds, s, L);
 }
 
 template <int MAXT>
