@@ -31,6 +31,7 @@
 
 #include "cx_down.h"
 #include "cx_gate_up.h"
+#include "cx_grouped.h"
 
 namespace cx {
 namespace {
@@ -452,6 +453,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 }
 
 // ---------------------------------------------------------------------------
+// Grouped GEMM for items of up to 64 pairs (cx_grouped.h): gate/up over
+// grid = (inter/64, items), down over grid = (hidden/256, items).  LDS rings
+// of 80 KB / 128 KB: two gate/up or one down workgroup per CU.
+template <int NKB, bool F16, bool SINGLE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_gu_grp(ExpertLaunch L) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char grp_lds[];
+    grp_gate_up_tile<NKB, F16, SINGLE>(L, blockIdx.x, blockIdx.y, grp_lds);
+}
+
+template <int NKB, bool SINGLE>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k_dn_grp(ExpertLaunch L) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char grp_lds[];
+    grp_down_tile<NKB, SINGLE>(L, blockIdx.x, blockIdx.y, grp_lds);
+}
+
+// ---------------------------------------------------------------------------
 // Combine: y[t] = sum_k w_k * y_part[pair(t,k)]  (route order, fp32)
 //               + y_part[pair(t, shared)]
 // then cast (RNE).  One thread per 4 consecutive features.
@@ -667,11 +684,51 @@ bool pick_down(const ExpertLaunch& L, dim3 grid, hipStream_t s) {
     }
 }
 
+// The grouped GEMM serves items of up to 64 pairs when the device grants its
+// LDS rings and the shape tiles evenly.
+bool grp_ok(const ExpertLaunch& L) {
+    return L.maxt == 4 && L.max_lds >= (int)grp_dn_lds() && L.inter % kGuGrpRows == 0 &&
+           L.hidden % kDnGrpRows == 0 && L.hidden / kKB <= 64 && L.inter / kKB <= 64;
+}
+
+template <int NKB, bool F16>
+void go_gu_grp(const ExpertLaunch& L, dim3 grid, hipStream_t s) {
+    if (L.table == nullptr) cx_launch((k_gu_grp<NKB, F16, true>), grid, dim3(256), grp_gu_lds(), s, L);
+    else cx_launch((k_gu_grp<NKB, F16, false>), grid, dim3(256), grp_gu_lds(), s, L);
+}
+
+bool pick_gu_grp(const ExpertLaunch& L, int items, hipStream_t s) {
+    const dim3 grid(L.inter / kGuGrpRows, items);
+    const bool f16 = L.in_dtype == CX_DTYPE_FP16;
+    switch (L.hidden / kKB) {
+        case 56: f16 ? go_gu_grp<56, true>(L, grid, s) : go_gu_grp<56, false>(L, grid, s); return true;
+        case 4: f16 ? go_gu_grp<4, true>(L, grid, s) : go_gu_grp<4, false>(L, grid, s); return true;
+        case 8: f16 ? go_gu_grp<8, true>(L, grid, s) : go_gu_grp<8, false>(L, grid, s); return true;
+        default: return false;
+    }
+}
+
+template <int NKB>
+void go_dn_grp(const ExpertLaunch& L, dim3 grid, hipStream_t s) {
+    if (L.table == nullptr) cx_launch((k_dn_grp<NKB, true>), grid, dim3(512), grp_dn_lds(), s, L);
+    else cx_launch((k_dn_grp<NKB, false>), grid, dim3(512), grp_dn_lds(), s, L);
+}
+
+bool pick_dn_grp(const ExpertLaunch& L, int items, hipStream_t s) {
+    const dim3 grid(L.hidden / kDnGrpRows, items);
+    switch (L.inter / kKB) {
+        case 16: go_dn_grp<16>(L, grid, s); return true;
+        case 4: go_dn_grp<4>(L, grid, s); return true;
+        default: return false;
+    }
+}
+
 }  // namespace
 
 hipError_t launch_gate_up(const ExpertLaunch& L, hipStream_t s) {
     const int items = L.table != nullptr ? L.max_items
                                          : (L.n_tokens + kTileTok * L.maxt - 1) / (kTileTok * L.maxt);
+    if (grp_ok(L) && pick_gu_grp(L, items, s)) return hipGetLastError();
     const dim3 grid(L.inter / kTileRows, items);
     const bool f16 = L.in_dtype == CX_DTYPE_FP16;
     bool done;
@@ -692,6 +749,7 @@ hipError_t launch_gate_up(const ExpertLaunch& L, hipStream_t s) {
 hipError_t launch_down(const ExpertLaunch& L, hipStream_t s) {
     const int items = L.table != nullptr ? L.max_items
                                          : (L.n_tokens + kTileTok * L.maxt - 1) / (kTileTok * L.maxt);
+    if (grp_ok(L) && pick_dn_grp(L, items, s)) return hipGetLastError();
     const dim3 grid(L.hidden / (kTileRows * kWaves), items);
     const bool done = L.maxt == 1 ? pick_down<1>(L, grid, s) : pick_down<4>(L, grid, s);
     if (!done) {

@@ -1,0 +1,362 @@
+// cx_grouped.h — the grouped fp8 expert MLP for work items of up to 64
+// pairs (prefill chunks and large decode batches): gate/up + SiLU and the
+// down projection as two MFMA GEMM kernels over (row tile, item).
+// Semantics: RunFusedUpGateReferenceV2 / RunDownReferenceV2
+// (expert_node_v2/backend/expert_reference_v2.cc:11-144) per expert,
+// dequantise-then-fp32, h kept to 16 significant bits (bf16 hi + lo).
+//
+// Why this shape.  The activations of an item (x rows for gate/up, h rows for
+// down) are shared by every weight row of the tile, so they go through LDS.
+// For each 128-column k-block, the workgroup's waves each load one quarter
+// (one "piece") of the item's activation block into registers.  They issue
+// it together with that k-block's weights, D k-blocks ahead, in the same
+// register ring.  Just before the k-block is used, the pieces are written
+// to one of two LDS slots and a barrier publishes them.  Every vector load
+// in the loop is an ordinary load of the same kind, so the in-order vmcnt
+// wait that makes a k-block's weights usable also covers its activations.
+// The compiler keeps exact waits across the rolled loop.  Direct
+// global->LDS loads would instead mark the counter out of order and drain
+// it at every loop header.
+//
+#pragma once
+
+#include "cx_gate_up.h"
+
+namespace cx {
+
+constexpr int kGrpTiles = 4;                         // 16-pair column tiles per item
+constexpr int kGrpPairs = kTileTok * kGrpTiles;      // 64 pairs per item
+constexpr size_t kPiece = 1024;                      // one wave load (64 x 16 B)
+constexpr size_t kActBlk = 4 * kPiece;               // 16 pairs x 128 k x 16 bit
+
+// gate/up: 4 waves x 16 rows of gate and of up, D-deep register ring; two
+// LDS slots of kGrpTiles activation blocks.
+constexpr int kGuGrpRows = kTileRows * kWaves;  // 64
+constexpr int kGuGrpD = 4;
+constexpr size_t grp_gu_lds() { return (size_t)2 * kGrpTiles * kActBlk; }  // 32 KB
+
+// down: 8 waves x 32 rows (two 16-row MFMA tiles sharing each B fragment);
+// h enters as two planes (hi, lo), so a slot holds 2 x kGrpTiles blocks.
+constexpr int kDnGrpWaves = 8;
+constexpr int kDnGrpRows = kDnGrpWaves * 2 * kTileRows;  // 256
+constexpr int kDnGrpD = 3;
+constexpr size_t grp_dn_lds() { return (size_t)2 * 2 * kGrpTiles * kActBlk; }  // 64 KB
+
+// Barrier after this wave's LDS writes: the writes complete (lgkmcnt), no
+// wait on vector memory loads (a release fence on all memory would drain
+// the weight ring).
+__device__ __forceinline__ void lds_write_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Scale of k-block k of the lane-distributed scale row `v` (lane l holds
+// k-block l).
+__device__ __forceinline__ float lane_scale(float v, int k) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), k));
+}
+
+// Wait for the stage issued W stages back (W = stages issued after it, each
+// of PS loads): a compile-time count for s_waitcnt.
+template <int PS>
+__device__ __forceinline__ void wait_stages(int later) {
+    if (later >= 3) vm_wait<3 * PS>();
+    else if (later == 2) vm_wait<2 * PS>();
+    else if (later == 1) vm_wait<PS>();
+    else vm_wait<0>();
+}
+
+// The streaming loop shared by both kernels: a prologue of D stages, then
+// NKB steps of [wait for stage k; publish its activations; compute k; issue
+// stage k + D].  The steady part runs as a rolled loop of D-step bodies so
+// every ring index and LDS slot (k % D, k % 2) is a compile-time constant.
+// `issue(k, s)`, `publish(s, slot)` and `compute(k, s, slot)` are the
+// kernel's stage actions.
+template <int NKB, int D, int PS, class Issue, class Publish, class Compute>
+__device__ __forceinline__ void grp_stream(Issue&& issue, Publish&& publish, Compute&& compute) {
+    static_assert(D % 2 == 0 || NKB <= D, "LDS slot k % 2 must be fixed per ring stage");
+    static_assert((D - 1) * PS < 64, "vmcnt range");
+    // the prologue keeps stage order (the loop's waits assume it)
+#pragma unroll
+    for (int k = 0; k < D && k < NKB; ++k) {
+        issue(k, k);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    constexpr int NST = NKB > D ? NKB - D : 0;  // steps that issue a stage
+    constexpr int NCH = NST / D;
+    int k0 = 0;
+#pragma unroll 1
+    for (int ch = 0; ch < NCH; ++ch, k0 += D) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            vm_wait<(D - 1) * PS>();
+            publish(i, i & 1);
+            lds_write_barrier();
+            compute(k0 + i, i, i & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            issue(k0 + i + D, i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NST % D; ++i) {
+        const int k = NCH * D + i;
+        vm_wait<(D - 1) * PS>();
+        publish(k % D, k & 1);
+        lds_write_barrier();
+        compute(k, k % D, k & 1);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(k + D, k % D);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    constexpr int NTAIL = NKB < D ? NKB : D;
+#pragma unroll
+    for (int i = 0; i < NTAIL; ++i) {
+        const int k = NST + i;
+        wait_stages<PS>(NTAIL - 1 - i);
+        publish(k % D, k & 1);
+        lds_write_barrier();
+        compute(k, k % D, k & 1);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// gate/up.  NKB = hidden / 128 k-blocks (<= 64), NT = 16-pair column tiles
+// of this item (1..4, a compile-time branch per item).
+template <int NKB, int NT, bool F16, bool SINGLE>
+__device__ __forceinline__ void grp_gate_up_item(const ExpertLaunch& L, const Unit& u, int tile,
+                                                 unsigned char* lds) {
+    typedef Mma<F16> M;
+    typedef typename M::V V;
+    // short K (test shapes): a 2-deep ring keeps the steady-state loop a
+    // loop (a single-trip loop is flattened and the schedule then spills)
+    constexpr int D = NKB >= 12 ? kGuGrpD : 2;
+    constexpr int PS = 4 + NT;  // loads per stage per wave
+    constexpr size_t SLOT = (size_t)kGrpTiles * kActBlk;
+    static_assert(NKB <= 64, "scale row held one k-block per lane");
+    const int H = u.e.hidden, I = u.e.inter;
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int g = lane >> 4, c = lane & 15;
+    const int r0 = tile * kGuGrpRows + wave * kTileRows;
+    const size_t roff = (size_t)(r0 + c) * H + g * 32;
+    const uint8_t* pg = u.e.w_gate + roff;
+    const uint8_t* pu = u.e.w_up + roff;
+    const int rbg = __builtin_amdgcn_readfirstlane(r0 / u.e.gate_rb);
+    const int rbu = __builtin_amdgcn_readfirstlane(r0 / u.e.up_rb);
+    const float scg_v = lane < NKB ? ldf(u.e.s_gate + (size_t)rbg * NKB + lane) : 0.f;
+    const float scu_v = lane < NKB ? ldf(u.e.s_up + (size_t)rbu * NKB + lane) : 0.f;
+    // activation pieces: this wave loads piece j = wave of every column tile;
+    // lane (c, g) carries pair tt*16 + c, elements 8*(4g + wave) .. +7.
+    const uint16_t* xs[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+        const int q = min(tt * kTileTok + c, u.np - 1);
+        const int tok = SINGLE ? u.pb + q : ldi(L.plan.pair_token + u.pb + q);
+        xs[tt] = static_cast<const uint16_t*>(L.x) + (size_t)tok * H + 8 * (4 * g + wave);
+    }
+    u32x4 wb[D][4];
+    u32x4 xr[D][NT];
+    f32x4 accg[NT], accu[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+        accg[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        accu[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    auto issue = [&](int k, int s) {
+        wb[s][0] = ld16(pg + (size_t)k * kKB);
+        wb[s][1] = ld16(pg + (size_t)k * kKB + 16);
+        wb[s][2] = ld16(pu + (size_t)k * kKB);
+        wb[s][3] = ld16(pu + (size_t)k * kKB + 16);
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) xr[s][tt] = ld16(xs[tt] + (size_t)k * kKB);
+    };
+    auto publish = [&](int s, int slot) {
+        unsigned char* dst = lds + (size_t)slot * SLOT + wave * kPiece + lane * 16;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) *reinterpret_cast<u32x4*>(dst + tt * kActBlk) = xr[s][tt];
+    };
+    auto compute = [&](int k, int s, int slot) {
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        const float sgk = lane_scale(scg_v, k), suk = lane_scale(scu_v, k);
+        V ag[4], au[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            ag[j] = M::cvt(wb[s][j >> 1][(j & 1) * 2], wb[s][j >> 1][(j & 1) * 2 + 1]);
+            au[j] = M::cvt(wb[s][2 + (j >> 1)][(j & 1) * 2], wb[s][2 + (j >> 1)][(j & 1) * 2 + 1]);
+        }
+        const unsigned char* src = lds + (size_t)slot * SLOT + lane * 16;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) {
+            V bx[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                bx[j] = M::bits(*reinterpret_cast<const u32x4*>(src + tt * kActBlk + j * kPiece));
+            f32x4 tg = M::mma(ag[0], bx[0], zero);
+            f32x4 tu = M::mma(au[0], bx[0], zero);
+#pragma unroll
+            for (int j = 1; j < 4; ++j) {
+                tg = M::mma(ag[j], bx[j], tg);
+                tu = M::mma(au[j], bx[j], tu);
+            }
+            accg[tt] += sgk * tg;
+            accu[tt] += suk * tu;
+        }
+    };
+    grp_stream<NKB, D, PS>(issue, publish, compute);
+    // epilogue: h = SiLU(gate) * up as bf16 hi + lo (route weight folded in
+    // when the caller combines by plain sums)
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+        const int q = tt * kTileTok + c;
+        if (q < u.np) {
+            const size_t p = (size_t)(u.pb + q);
+            const float wf = !SINGLE && L.fold_weight ? L.plan.pair_weight[p] : 1.0f;
+            const int row = r0 + 4 * g;
+            uint32_t hi[4], lo[4];
+            float hv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float gate = accg[tt][i], up = accu[tt][i];
+                const float h = (gate / (1.0f + expf(-gate))) * up;
+                hv[i] = h;
+                const float hw = h * wf;
+                hi[i] = bf16_rne(hw);
+                lo[i] = bf16_rne(hw - __uint_as_float(hi[i] << 16));
+            }
+            *reinterpret_cast<uint2*>(L.h_hi + p * I + row) = uint2{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
+            *reinterpret_cast<uint2*>(L.h_lo + p * I + row) = uint2{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
+            if (L.h_f32 != nullptr)
+                *reinterpret_cast<float4*>(L.h_f32 + p * I + row) = float4{hv[0], hv[1], hv[2], hv[3]};
+        }
+    }
+}
+
+template <int NKB, bool F16, bool SINGLE>
+__device__ __forceinline__ void grp_gate_up_tile(const ExpertLaunch& L, int tile, int item,
+                                                 unsigned char* lds) {
+    Unit u;
+    if (!resolve_unit<SINGLE>(L, item, kGrpPairs, &u)) return;
+    const int nt = (u.np + kTileTok - 1) / kTileTok;  // uniform: one branch per item
+    if (nt == 1) grp_gate_up_item<NKB, 1, F16, SINGLE>(L, u, tile, lds);
+    else if (nt == 2) grp_gate_up_item<NKB, 2, F16, SINGLE>(L, u, tile, lds);
+    else if (nt == 3) grp_gate_up_item<NKB, 3, F16, SINGLE>(L, u, tile, lds);
+    else grp_gate_up_item<NKB, 4, F16, SINGLE>(L, u, tile, lds);
+}
+
+// ---------------------------------------------------------------------------
+// down.  NKB = inter / 128 k-blocks (<= 64).  Each wave owns 32 rows of Wd
+// (two MFMA row tiles) and reads each h fragment once for both.
+template <int NKB, int NT, bool SINGLE>
+__device__ __forceinline__ void grp_down_item(const ExpertLaunch& L, const Unit& u, int tile,
+                                              unsigned char* lds) {
+    typedef Mma<false> M;
+    typedef M::V V;
+    constexpr int D = NKB >= 8 ? 4 : 2;
+    constexpr int PS = 4 + NT;
+    constexpr size_t PLANE = (size_t)kGrpTiles * kActBlk;
+    constexpr size_t SLOT = 2 * PLANE;
+    static_assert(NKB <= 64, "scale row held one k-block per lane");
+    const int H = u.e.hidden, I = u.e.inter;
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int g = lane >> 4, c = lane & 15;
+    const int rw = tile * kDnGrpRows + wave * (2 * kTileRows);
+    const uint8_t* pd = u.e.w_down + (size_t)(rw + c) * I + g * 32;
+    const size_t pd1 = (size_t)kTileRows * I;  // second row tile
+    const int rb0 = __builtin_amdgcn_readfirstlane(rw / u.e.down_rb);
+    const int rb1 = __builtin_amdgcn_readfirstlane((rw + kTileRows) / u.e.down_rb);
+    const float sd0_v = lane < NKB ? ldf(u.e.s_down + (size_t)rb0 * NKB + lane) : 0.f;
+    const float sd1_v = lane < NKB ? ldf(u.e.s_down + (size_t)rb1 * NKB + lane) : 0.f;
+    // h pieces: wave w loads plane w / 4 (hi, lo), piece j = w % 4 of every
+    // column tile.
+    const int plane = wave >> 2, pj = wave & 3;
+    const uint16_t* hs[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+        const int q = min(tt * kTileTok + c, u.np - 1);
+        hs[tt] = (plane ? L.h_lo : L.h_hi) + (size_t)(u.pb + q) * I + 8 * (4 * g + pj);
+    }
+    u32x4 wb[D][4];
+    u32x4 hr[D][NT];
+    f32x4 acc[2][NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+        acc[0][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc[1][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    auto issue = [&](int k, int s) {
+        wb[s][0] = ld16(pd + (size_t)k * kKB);
+        wb[s][1] = ld16(pd + (size_t)k * kKB + 16);
+        wb[s][2] = ld16(pd + pd1 + (size_t)k * kKB);
+        wb[s][3] = ld16(pd + pd1 + (size_t)k * kKB + 16);
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) hr[s][tt] = ld16(hs[tt] + (size_t)k * kKB);
+    };
+    auto publish = [&](int s, int slot) {
+        unsigned char* dst = lds + (size_t)slot * SLOT + plane * PLANE + pj * kPiece + lane * 16;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) *reinterpret_cast<u32x4*>(dst + tt * kActBlk) = hr[s][tt];
+    };
+    auto compute = [&](int k, int s, int slot) {
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        const float s0 = lane_scale(sd0_v, k), s1 = lane_scale(sd1_v, k);
+        V a0[4], a1[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            a0[j] = M::cvt(wb[s][j >> 1][(j & 1) * 2], wb[s][j >> 1][(j & 1) * 2 + 1]);
+            a1[j] = M::cvt(wb[s][2 + (j >> 1)][(j & 1) * 2], wb[s][2 + (j >> 1)][(j & 1) * 2 + 1]);
+        }
+        const unsigned char* src = lds + (size_t)slot * SLOT + lane * 16;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) {
+            V bh[4], bl[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                bh[j] = M::bits(*reinterpret_cast<const u32x4*>(src + tt * kActBlk + j * kPiece));
+                bl[j] = M::bits(*reinterpret_cast<const u32x4*>(src + PLANE + tt * kActBlk + j * kPiece));
+            }
+            f32x4 t0 = M::mma(a0[0], bh[0], zero);
+            f32x4 t1 = M::mma(a1[0], bh[0], zero);
+            t0 = M::mma(a0[0], bl[0], t0);
+            t1 = M::mma(a1[0], bl[0], t1);
+#pragma unroll
+            for (int j = 1; j < 4; ++j) {
+                t0 = M::mma(a0[j], bh[j], t0);
+                t1 = M::mma(a1[j], bh[j], t1);
+                t0 = M::mma(a0[j], bl[j], t0);
+                t1 = M::mma(a1[j], bl[j], t1);
+            }
+            acc[0][tt] += s0 * t0;
+            acc[1][tt] += s1 * t1;
+        }
+    };
+    grp_stream<NKB, D, PS>(issue, publish, compute);
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+        const int row = rw + a * kTileRows + 4 * g;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) {
+            const int q = tt * kTileTok + c;
+            if (q < u.np) {
+                const size_t p = (size_t)(u.pb + q);
+                const f32x4 v = acc[a][tt];
+                if (SINGLE) store_out4(L.y, L.y_f32, p * H + row, v, L.out_dtype);
+                else *reinterpret_cast<float4*>(L.y_part + p * H + row) = float4{v[0], v[1], v[2], v[3]};
+            }
+        }
+    }
+}
+
+template <int NKB, bool SINGLE>
+__device__ __forceinline__ void grp_down_tile(const ExpertLaunch& L, int tile, int item,
+                                              unsigned char* lds) {
+    Unit u;
+    if (!resolve_unit<SINGLE>(L, item, kGrpPairs, &u)) return;
+    const int nt = (u.np + kTileTok - 1) / kTileTok;
+    if (nt == 1) grp_down_item<NKB, 1, SINGLE>(L, u, tile, lds);
+    else if (nt == 2) grp_down_item<NKB, 2, SINGLE>(L, u, tile, lds);
+    else if (nt == 3) grp_down_item<NKB, 3, SINGLE>(L, u, tile, lds);
+    else grp_down_item<NKB, 4, SINGLE>(L, u, tile, lds);
+}
+
+}  // namespace cx

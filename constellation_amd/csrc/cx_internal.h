@@ -140,6 +140,7 @@ struct ExpertLaunch {
     int fold_weight;              // phase A multiplies h by the pair's route weight
     int np_lds;                   // >0: stage up to np_lds activation rows per item in LDS
     int skip_shared;              // grouped mode: routed items only (shared expert done apart)
+    int max_lds;                  // dynamic LDS per workgroup the device allows (0: unknown)
 };
 
 hipError_t launch_gate_up(const ExpertLaunch& L, hipStream_t s);

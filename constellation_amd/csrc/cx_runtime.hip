@@ -498,6 +498,7 @@ int moe_run(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int
     L.y_f32 = y_f32;
     L.out_dtype = out_dtype;
     L.np_lds = z.maxt == 1 ? lds_rows(ctx, layer->hidden, std::min(n_tokens, z.item_cap)) : 0;
+    L.max_lds = ctx->max_lds;
     {
         Span sp(ctx, "gate_up", s);
         CX_HIP(launch_gate_up(L, s));
@@ -768,6 +769,7 @@ int cx_expert_run(cx_ctx* ctx, const cx_expert_desc* expert, const void* x, int 
     L.y_f32 = y_f32;
     L.out_dtype = out_dtype;
     L.np_lds = L.maxt == 1 ? lds_rows(ctx, expert->hidden, n_tokens) : 0;
+    L.max_lds = ctx->max_lds;
     {
         Span sp(ctx, "gate_up", s);
         CX_HIP(launch_gate_up(L, s));

@@ -342,3 +342,44 @@ def test_full_size_moe_layer(gpu, oracle, T):
         assert np.array_equal(_bits(y), oracle.encode_act(yf, BF16, "rne"))
     finally:
         _free(layer, experts, sh)
+
+
+def test_full_size_prefill_grouped_items(gpu, oracle):
+    """The grouped GEMM at DeepSeek-V3 shapes (H=7168, I=2048) with items of
+    every width: expert 0 takes all 72 tokens (items of 64 + 8 pairs), expert 1
+    40 (3 column tiles), expert 2 20 (2 tiles), the rest a few each; shared
+    expert on.  The oracle checks a sample of tokens spread over the items."""
+    print("[moe] full-size prefill items", flush=True)
+    E, H, I, T, K = 16, 7168, 2048, 72, 4
+    from constellation_amd.engine import Expert, Layer
+    experts = [Expert.generate(0, 91, 0x4000 + 4 * e) for e in range(E)]
+    sh = Expert.generate(0, 91, 0x4000 + 4 * E)
+    layer = Layer(gpu, experts, sh)
+    try:
+        x = gpu.gen_normal(92, 1, (T, H), 1.0, torch.bfloat16)
+        rng = np.random.default_rng(93)
+        ids = np.full((T, K), -1, np.int32)
+        for t in range(T):
+            row = [0]
+            if t < 40:
+                row.append(1)
+            if t % 3 == 0 and len(row) < K:
+                row.append(2)
+            rest = rng.choice(np.arange(3, E), K - len(row), replace=False)
+            ids[t] = row + rest.tolist()
+        wts = rng.uniform(0.05, 1.0, ids.shape).astype(np.float32)
+        y, yf = gpu.moe(layer, x, torch.from_numpy(ids).cuda(), torch.from_numpy(wts).cuda(),
+                        want_f32=True, prefill=True)
+        gpu.sync()
+        sel = np.array([0, 17, 39, 45, 63, 64, 71])
+        used = sorted(set(ids[sel].ravel().tolist()))
+        cpu = {e: oracle.gen_expert(91, 0x4000 + 4 * e) for e in used}
+        cpu_sh = oracle.gen_expert(91, 0x4000 + 4 * E)
+        ref = _oracle_moe(oracle, [cpu.get(e) for e in range(E)], cpu_sh,
+                          x.float().cpu().numpy()[sel], ids[sel], wts[sel])
+        yf = yf.cpu().numpy()[sel]
+        assert rel_l2(yf, ref) < 1e-5, rel_l2(yf, ref)
+        assert np.abs(yf - ref).max() < 2e-2
+        assert np.array_equal(_bits(y)[sel], oracle.encode_act(yf, BF16, "rne"))
+    finally:
+        _free(layer, experts, sh)
