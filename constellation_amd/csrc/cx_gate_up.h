@@ -2,8 +2,9 @@
 // as a device function so that both the stand-alone gate/up kernel and the
 // decode kernels that overlap the shared expert with the router can run it.
 //
-// One workgroup tile = 16 rows of gate and up of one expert for all pairs of
-// one work item (<= 16*MAXT), K split over the KS waves; the partial tiles
+// One workgroup tile = TR (16, or 8 to spread a small grid over more CUs)
+// rows of gate and up of one expert for all pairs of one work item
+// (<= 16*MAXT), K split over the KS waves; the partial tiles
 // are summed in LDS in a fixed order and the SiLU(gate)*up epilogue writes h
 // as a bf16 hi/lo split (h = hi + lo to 2^-17 relative).
 // Semantics: RunFusedUpGateReferenceV2 (expert_node_v2/backend/
@@ -91,7 +92,7 @@ inline size_t gate_up_lds_bytes(int ksa, int maxt, int np_lds, int hidden) {
     return gate_up_red_bytes(ksa, maxt) + (maxt == 1 ? (size_t)np_lds * ((size_t)hidden * 2 + 16) : 0);
 }
 
-template <int NKB, int D, int MAXT, bool F16, bool XLDS, int KS, bool SINGLE, int KSA = KS>
+template <int NKB, int D, int MAXT, bool F16, bool XLDS, int KS, bool SINGLE, int KSA = KS, int TR = kTileRows>
 __device__ __forceinline__ void gate_up_tile(const ExpertLaunch& L, int tile, int item,
                                              unsigned char* lds) {
     typedef Mma<F16> M;
@@ -101,13 +102,16 @@ __device__ __forceinline__ void gate_up_tile(const ExpertLaunch& L, int tile, in
     Unit u;
     if (!resolve_unit<SINGLE>(L, item, kTileTok * MAXT, &u)) return;
     const int H = u.e.hidden, I = u.e.inter;
-    const int r0 = tile * kTileRows;
+    static_assert(TR == 16 || TR == 8, "tile rows");
+    const int r0 = tile * TR;
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int g = lane >> 4, c = lane & 15;
     const bool active = KSA == KS || wave < KSA;  // wave-uniform
     const int kb0 = (active ? wave : 0) * NKB;
 
-    const size_t roff = (size_t)(r0 + c) * H + (size_t)kb0 * kKB + g * 32;
+    // TR = 8: lanes c and c + 8 read the same row (one fetch per wave
+    // instruction); MFMA rows 8..15 are discarded
+    const size_t roff = (size_t)(r0 + (c & (TR - 1))) * H + (size_t)kb0 * kKB + g * 32;
     const uint8_t* pg = u.e.w_gate + roff;
     const uint8_t* pu = u.e.w_up + roff;
     // integer division runs on the VALU: pin the (uniform) results to SGPRs
@@ -251,7 +255,7 @@ __device__ __forceinline__ void gate_up_tile(const ExpertLaunch& L, int tile, in
             U += red[((w * MAXT + tt) * 2 + 1) * 64 + lane];
         }
         const int q = tt * kTileTok + c;
-        if (q < u.np) {
+        if (q < u.np && 4 * g < TR) {
             const size_t p = (size_t)(u.pb + q);
             const float wf = !SINGLE && L.fold_weight ? L.plan.pair_weight[p] : 1.0f;
             const int row = r0 + 4 * g;

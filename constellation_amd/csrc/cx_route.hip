@@ -9,7 +9,8 @@
 //
 // Launch shapes
 //  * cx_route / general path: k_route_logits (one workgroup per expert row
-//    streams W_r once for up to 16 tokens), then k_route_select_small
+//    streams W_r once for up to 16 tokens; k_route_logits_mfma on the fp64
+//    matrix cores from 32 tokens up), then k_route_select_small
 //    (T <= 16, one workgroup) or k_route_select (4 tokens per workgroup),
 //    then, for the grouped MoE, k_plan.
 //  * decode pipeline (T <= 16, E <= 256):
@@ -1019,6 +1020,119 @@ __global__ __launch_bounds__(kRouteThreads) void k_route_logits(FusedArgs A) {
                            A.logits, red);
 }
 
+// Router logits for many tokens on the fp64 matrix cores
+// (v_mfma_f64_16x16x4_f64).  Workgroup tile = 16 experts x 32 tokens, the 8
+// waves split K and their partial tiles are summed in LDS in a fixed order.
+// Products of bf16 (or fp32) values are exact in fp64, so the logits equal
+// the sequential fp64 sums of exact products up to fp64 summation order
+// (relative 1e-15), far inside the 1e-12 margin below which a selection is
+// treated as a tie.  MFMA operand layout: lane (i = lane % 16, g = lane / 16)
+// holds A[i][g] and B[g][i]; here A = W rows (experts), B = x^T (tokens).
+// The lane loads 8 consecutive k of its rows per 32-k chunk and feeds
+// element s to MFMA step s, so step s covers k = k0 + 8g + s for all g.
+// Chunks stream through a 4-deep register ring (L2 latency is the bound).
+constexpr int kLgE = 16;       // experts per workgroup tile
+constexpr int kLgT = 32;       // tokens per workgroup tile (two MFMA column tiles)
+constexpr int kLgWaves = 8;    // K split
+constexpr int kLgRing = 4;     // chunks in flight per wave
+constexpr int kLgMinTokens = 32;
+
+bool logits_mfma_ok(int n_tokens, int hidden) {
+    return n_tokens >= kLgMinTokens && hidden % (kLgWaves * 32 * kLgRing) == 0;
+}
+
+// 8 elements (bf16: one dwordx4; fp32: two) widened to fp64 (exact).
+template <bool F32>
+struct Raw8 {
+    u32x4 a, b;
+    __device__ __forceinline__ void load(const void* base, size_t elem) {
+        if (F32) {
+            const float* p = static_cast<const float*>(base) + elem;
+            a = ld16(p);
+            b = ld16(p + 4);
+        } else {
+            a = ld16(static_cast<const uint16_t*>(base) + elem);
+        }
+    }
+    __device__ __forceinline__ double get(int i) const {
+        if (F32) return static_cast<double>(__uint_as_float(i < 4 ? a[i] : b[i - 4]));
+        const uint32_t w = a[i >> 1];
+        return static_cast<double>(__uint_as_float((i & 1) ? (w & 0xFFFF0000u) : (w << 16)));
+    }
+};
+
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+template <bool XF32, bool WF32>
+__global__ __launch_bounds__(64 * kLgWaves) void k_route_logits_mfma(FusedArgs A) {
+    __shared__ double red[kLgWaves][2][4][64];
+    const int E = A.n_experts, T = A.n_tokens, H = A.hidden;
+    const int e0 = blockIdx.x * kLgE, t0 = blockIdx.y * kLgT;
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int i = lane & 15, g = lane >> 4;
+    const int kw = H / kLgWaves;  // k per wave, a multiple of 32 * kLgRing
+    const size_t kb = (size_t)wave * kw + 8 * g;
+    const size_t wr = (size_t)min(e0 + i, E - 1) * H + kb;
+    const size_t xa = (size_t)min(t0 + i, T - 1) * H + kb;
+    const size_t xb = (size_t)min(t0 + kTileTok + i, T - 1) * H + kb;
+    f64x4 acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
+    Raw8<WF32> ra[kLgRing];
+    Raw8<XF32> rb0[kLgRing], rb1[kLgRing];
+    auto issue = [&](int c, int s) {
+        ra[s].load(A.w, wr + (size_t)c * 32);
+        rb0[s].load(A.x, xa + (size_t)c * 32);
+        rb1[s].load(A.x, xb + (size_t)c * 32);
+    };
+    auto comp = [&](int s) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const double a = ra[s].get(e);
+            acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(a, rb0[s].get(e), acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(a, rb1[s].get(e), acc1, 0, 0, 0);
+        }
+    };
+#pragma unroll
+    for (int s = 0; s < kLgRing; ++s) {
+        issue(s, s);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const int nch = kw / 32;
+#pragma unroll 1
+    for (int c = 0; c < nch - kLgRing; c += kLgRing) {
+#pragma unroll
+        for (int s = 0; s < kLgRing; ++s) {
+            comp(s);
+            __builtin_amdgcn_sched_barrier(0);
+            issue(c + kLgRing + s, s);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < kLgRing; ++s) comp(s);
+    // the f64 16x16 result layout: lane (i, g) element r holds D[g + 4r][i]
+    // (expert e0 + g + 4r, token t0 (+16) + i), unlike the 16-bit MFMAs'
+    // D[4g + r][i]
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        red[wave][0][r][lane] = acc0[r];
+        red[wave][1][r][lane] = acc1[r];
+    }
+    __syncthreads();
+    const int tid = threadIdx.x;
+    if (tid < 2 * 64) {
+        const int tt = tid >> 6, l = tid & 63;
+        const int t = t0 + tt * kTileTok + (l & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int e = e0 + (l >> 4) + 4 * r;
+            double v = red[0][tt][r][l];
+#pragma unroll
+            for (int w = 1; w < kLgWaves; ++w) v += red[w][tt][r][l];
+            if (t < T && e < E) A.logits[(size_t)t * E + e] = v;
+        }
+    }
+}
+
 // T <= 16, selection only: wave t selects token t (register path: all tokens
 // in parallel; LDS fallback: 4 waves loop over the tokens).
 __global__ __launch_bounds__(1024) void k_route_select_small(FusedArgs A) {
@@ -1322,12 +1436,23 @@ hipError_t launch_route(const RouteArgs& R, hipStream_t s) {
     FusedArgs A = fused_args(R);
     A.epl = register_epl(R.n_experts, R.n_group);
     const size_t sel = A.epl ? 0 : select_lds(R.n_experts);
-    const dim3 lg(R.n_experts, (R.n_tokens + kRouteTB - 1) / kRouteTB);
     const bool xf = R.x_dtype == CX_DTYPE_F32, wf = R.w_dtype == CX_DTYPE_F32;
-    if (xf && wf) cx_launch((k_route_logits<true, true>), lg, dim3(kRouteThreads), 0, s, A);
-    else if (xf) cx_launch((k_route_logits<true, false>), lg, dim3(kRouteThreads), 0, s, A);
-    else if (wf) cx_launch((k_route_logits<false, true>), lg, dim3(kRouteThreads), 0, s, A);
-    else cx_launch((k_route_logits<false, false>), lg, dim3(kRouteThreads), 0, s, A);
+    if (logits_mfma_ok(R.n_tokens, R.hidden)) {
+        // many tokens: fp64 MFMA tiles
+        const dim3 lg((R.n_experts + kLgE - 1) / kLgE, (R.n_tokens + kLgT - 1) / kLgT);
+        const dim3 blk(64 * kLgWaves);
+        if (xf && wf) cx_launch((k_route_logits_mfma<true, true>), lg, blk, 0, s, A);
+        else if (xf) cx_launch((k_route_logits_mfma<true, false>), lg, blk, 0, s, A);
+        else if (wf) cx_launch((k_route_logits_mfma<false, true>), lg, blk, 0, s, A);
+        else cx_launch((k_route_logits_mfma<false, false>), lg, blk, 0, s, A);
+    } else {
+        // few tokens: one workgroup per expert row streams W_r once
+        const dim3 lg(R.n_experts, (R.n_tokens + kRouteTB - 1) / kRouteTB);
+        if (xf && wf) cx_launch((k_route_logits<true, true>), lg, dim3(kRouteThreads), 0, s, A);
+        else if (xf) cx_launch((k_route_logits<true, false>), lg, dim3(kRouteThreads), 0, s, A);
+        else if (wf) cx_launch((k_route_logits<false, true>), lg, dim3(kRouteThreads), 0, s, A);
+        else cx_launch((k_route_logits<false, false>), lg, dim3(kRouteThreads), 0, s, A);
+    }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     if (R.n_tokens <= kRouteTB) {

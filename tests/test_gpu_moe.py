@@ -43,7 +43,8 @@ def _oracle_route(oracle, x, w, bias, **kw):
 
 
 @pytest.mark.parametrize("T,E,H,G,TG,K", [(1, 256, 7168, 8, 4, 8), (16, 256, 7168, 8, 4, 8),
-                                          (37, 64, 512, 8, 4, 6), (5, 32, 256, 4, 2, 3)])
+                                          (37, 64, 512, 8, 4, 6), (5, 32, 256, 4, 2, 3),
+                                          (96, 256, 7168, 8, 4, 8), (45, 72, 1024, 8, 4, 6)])
 def test_router_vs_oracle(gpu, oracle, T, E, H, G, TG, K):
     print(f"[route] T={T} E={E} H={H}", flush=True)
     x, w, bias = _router_inputs(gpu, 100 + T, T, E, H)
@@ -55,6 +56,26 @@ def test_router_vs_oracle(gpu, oracle, T, E, H, G, TG, K):
         if min(margins) <= 1e-12:
             continue  # exact-math tie: order undefined
         assert ids[t].tolist() == oi.tolist(), t  # same set and same (descending) order
+        assert np.allclose(wts[t], ow, rtol=1e-6, atol=0), t
+
+
+@pytest.mark.parametrize("xdt,wdt", [(torch.float32, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                     (torch.float32, torch.float32)])
+def test_router_many_tokens_fp32_operands(gpu, oracle, xdt, wdt):
+    """The fp64-MFMA logits path (T >= 32) with fp32 activations or weights:
+    products of fp32 values are exact in fp64 too."""
+    print(f"[route] T=40 x={xdt} w={wdt}", flush=True)
+    T, E, H = 40, 64, 2048
+    x, w, bias = _router_inputs(gpu, 300, T, E, H)
+    x = (x.float() * 1.37).to(xdt)   # fp32 values with more than 8 significant bits
+    w = (w.float() * 0.73).to(wdt)
+    ids, wts = gpu.route(x, w, bias, n_group=8, topk_group=4, top_k=8)
+    torch.cuda.synchronize()
+    ids, wts = ids.cpu().numpy(), wts.cpu().numpy()
+    for t, (oi, ow, margins, _) in enumerate(_oracle_route(oracle, x, w, bias)):
+        if min(margins) <= 1e-12:
+            continue
+        assert ids[t].tolist() == oi.tolist(), t
         assert np.allclose(wts[t], ow, rtol=1e-6, atol=0), t
 
 
