@@ -72,9 +72,10 @@ __device__ __forceinline__ void wait_stages(int later) {
 // stage k + D].  The steady part runs as a rolled loop of D-step bodies so
 // every ring index and LDS slot (k % D, k % 2) is a compile-time constant.
 // `issue(k, s)`, `publish(s, slot)` and `compute(k, s, slot)` are the
-// kernel's stage actions.
-template <int NKB, int D, int PS, class Issue, class Publish, class Compute>
-__device__ __forceinline__ void grp_stream(Issue&& issue, Publish&& publish, Compute&& compute) {
+// kernel's stage actions; `ready()` runs once the first stage has landed.
+template <int NKB, int D, int PS, class Issue, class Publish, class Compute, class Ready>
+__device__ __forceinline__ void grp_stream(Issue&& issue, Publish&& publish, Compute&& compute,
+                                           Ready&& ready) {
     static_assert(D % 2 == 0 || NKB <= D, "LDS slot k % 2 must be fixed per ring stage");
     static_assert((D - 1) * PS < 64, "vmcnt range");
     // the prologue keeps stage order (the loop's waits assume it)
@@ -83,6 +84,12 @@ __device__ __forceinline__ void grp_stream(Issue&& issue, Publish&& publish, Com
         issue(k, k);
         __builtin_amdgcn_sched_barrier(0);
     }
+    // stage 0 and every older load (the kernel's per-tile setup loads) have
+    // landed here; `ready` pins those values so that no later wait is
+    // computed for them (a loop-carried wait on them would drain the ring)
+    if (NKB > D) vm_wait<(D - 1) * PS>();
+    else vm_wait<0>();
+    ready();
     constexpr int NST = NKB > D ? NKB - D : 0;  // steps that issue a stage
     constexpr int NCH = NST / D;
     int k0 = 0;
@@ -102,6 +109,7 @@ __device__ __forceinline__ void grp_stream(Issue&& issue, Publish&& publish, Com
 #pragma unroll
     for (int i = 0; i < NST % D; ++i) {
         const int k = NCH * D + i;
+        __builtin_amdgcn_sched_barrier(0);
         vm_wait<(D - 1) * PS>();
         publish(k % D, k & 1);
         lds_write_barrier();
@@ -114,10 +122,13 @@ __device__ __forceinline__ void grp_stream(Issue&& issue, Publish&& publish, Com
 #pragma unroll
     for (int i = 0; i < NTAIL; ++i) {
         const int k = NST + i;
+        // keep each step's conversions below its own wait
+        __builtin_amdgcn_sched_barrier(0);
         wait_stages<PS>(NTAIL - 1 - i);
         publish(k % D, k & 1);
         lds_write_barrier();
         compute(k, k % D, k & 1);
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -144,8 +155,8 @@ __device__ __forceinline__ void grp_gate_up_item(const ExpertLaunch& L, const Un
     const uint8_t* pu = u.e.w_up + roff;
     const int rbg = __builtin_amdgcn_readfirstlane(r0 / u.e.gate_rb);
     const int rbu = __builtin_amdgcn_readfirstlane(r0 / u.e.up_rb);
-    const float scg_v = lane < NKB ? ldf(u.e.s_gate + (size_t)rbg * NKB + lane) : 0.f;
-    const float scu_v = lane < NKB ? ldf(u.e.s_up + (size_t)rbu * NKB + lane) : 0.f;
+    float scg_v = lane < NKB ? ldf(u.e.s_gate + (size_t)rbg * NKB + lane) : 0.f;
+    float scu_v = lane < NKB ? ldf(u.e.s_up + (size_t)rbu * NKB + lane) : 0.f;
     // activation pieces: this wave loads piece j = wave of every column tile;
     // lane (c, g) carries pair tt*16 + c, elements 8*(4g + wave) .. +7.
     const uint16_t* xs[NT];
@@ -203,7 +214,8 @@ __device__ __forceinline__ void grp_gate_up_item(const ExpertLaunch& L, const Un
             accu[tt] += suk * tu;
         }
     };
-    grp_stream<NKB, D, PS>(issue, publish, compute);
+    grp_stream<NKB, D, PS>(issue, publish, compute,
+                           [&] { asm volatile("" : "+v"(scg_v), "+v"(scu_v)); });
     // epilogue: h = SiLU(gate) * up as bf16 hi + lo (route weight folded in
     // when the caller combines by plain sums)
 #pragma unroll
@@ -265,8 +277,8 @@ __device__ __forceinline__ void grp_down_item(const ExpertLaunch& L, const Unit&
     const size_t pd1 = (size_t)kTileRows * I;  // second row tile
     const int rb0 = __builtin_amdgcn_readfirstlane(rw / u.e.down_rb);
     const int rb1 = __builtin_amdgcn_readfirstlane((rw + kTileRows) / u.e.down_rb);
-    const float sd0_v = lane < NKB ? ldf(u.e.s_down + (size_t)rb0 * NKB + lane) : 0.f;
-    const float sd1_v = lane < NKB ? ldf(u.e.s_down + (size_t)rb1 * NKB + lane) : 0.f;
+    float sd0_v = lane < NKB ? ldf(u.e.s_down + (size_t)rb0 * NKB + lane) : 0.f;
+    float sd1_v = lane < NKB ? ldf(u.e.s_down + (size_t)rb1 * NKB + lane) : 0.f;
     // h pieces: wave w loads plane w / 4 (hi, lo), piece j = w % 4 of every
     // column tile.
     const int plane = wave >> 2, pj = wave & 3;
@@ -330,7 +342,8 @@ __device__ __forceinline__ void grp_down_item(const ExpertLaunch& L, const Unit&
             acc[1][tt] += s1 * t1;
         }
     };
-    grp_stream<NKB, D, PS>(issue, publish, compute);
+    grp_stream<NKB, D, PS>(issue, publish, compute,
+                           [&] { asm volatile("" : "+v"(sd0_v), "+v"(sd1_v)); });
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
         const int row = rw + a * kTileRows + 4 * g;

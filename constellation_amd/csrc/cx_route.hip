@@ -806,6 +806,172 @@ __device__ __forceinline__ void plan_build(const int32_t* __restrict__ ids, cons
 
 constexpr int kPlanThreads = 1024;
 
+// Staged planner: the same plan as plan_build with every input first copied
+// into LDS in one round of independent loads (routes, layer table), so the
+// passes that follow wait only on LDS and the block barriers.  LDS layout:
+// table[E+1] | ids[n] | ok[n] | cnt[E] | cur[E] | scan[nt] | slot arrays
+// (expert, first pair, count) [E+1] each.
+size_t plan_staged_lds(int n_assign, int n_experts, int threads) {
+    return sizeof(cx_expert_desc) * ((size_t)n_experts + 1) +
+           sizeof(int) * (2 * (size_t)n_assign + 2 * (size_t)n_experts + threads +
+                          3 * ((size_t)n_experts + 1));
+}
+
+__device__ __forceinline__ void plan_build_staged(const int32_t* __restrict__ ids,
+                                                  const float* __restrict__ w, int n_tokens,
+                                                  int top_k, const cx_expert_desc* table,
+                                                  int n_experts, int has_shared, int item_cap,
+                                                  int max_items, const PlanPtrs& P, int* err_flag,
+                                                  unsigned char* lds) {
+    __shared__ int s_err;
+    const int E = n_experts, n_assign = n_tokens * top_k;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    cx_expert_desc* tab = reinterpret_cast<cx_expert_desc*>(lds);
+    int* sid = reinterpret_cast<int*>(tab + E + 1);
+    int* okv = sid + n_assign;
+    int* cnt = okv + n_assign;
+    int* cur = cnt + E;
+    int* scan = cur + E;
+    int* s_exp = scan + nt;
+    int* s_pb = s_exp + E + 1;
+    int* s_pc = s_pb + E + 1;
+    // 1) inputs -> LDS, one round of independent loads
+    {
+        constexpr int kChunks = sizeof(cx_expert_desc) / 16;
+        const u32x4* src = reinterpret_cast<const u32x4*>(table);
+        u32x4* dst = reinterpret_cast<u32x4*>(tab);
+        for (int i = tid; i < (E + 1) * kChunks; i += nt) dst[i] = ld16(src + i);
+        for (int i = tid; i < n_assign; i += nt) sid[i] = ldi(ids + i);
+        for (int e = tid; e < E; e += nt) cnt[e] = 0;
+        if (tid == 0) s_err = 0;
+    }
+    __syncthreads();
+    // 2) validity (range, residency, repeats within the token) and counts
+    for (int i = tid; i < n_assign; i += nt) {
+        const int e = sid[i];
+        int ok = 0;
+        if (e >= 0) {
+            if (e >= E) atomicOr(&s_err, kErrBadExpertId);
+            else if (tab[e].w_up == nullptr) atomicOr(&s_err, kErrNotResident);
+            else {
+                bool dup = false;
+                for (int j = (i / top_k) * top_k; j < i; ++j) dup |= sid[j] == e;
+                if (dup) atomicOr(&s_err, kErrDuplicateRoute);
+                else {
+                    ok = 1;
+                    atomicAdd(&cnt[e], 1);
+                }
+            }
+        }
+        okv[i] = ok;
+    }
+    __syncthreads();
+    // 3) slots in ascending expert id (block scans over per-thread ranges)
+    const bool shared = has_shared && tab[E].w_up != nullptr;
+    const int s0 = shared ? n_tokens : 0;  // first routed pair
+    const int chunk = (E + nt - 1) / nt;
+    const int e0 = min(tid * chunk, E), e1 = min(e0 + chunk, E);
+    int my_pairs = 0, my_slots = 0;
+    for (int e = e0; e < e1; ++e) {
+        my_pairs += cnt[e];
+        my_slots += cnt[e] > 0;
+    }
+    int tot_pairs = 0, tot_slots = 0;
+    int pair_off = s0 + block_excl_scan(my_pairs, scan, &tot_pairs);
+    int slot_off = block_excl_scan(my_slots, scan, &tot_slots);
+    for (int e = e0; e < e1; ++e) {
+        cur[e] = pair_off;
+        if (cnt[e] > 0) {
+            s_exp[slot_off] = e;
+            s_pb[slot_off] = pair_off;
+            s_pc[slot_off] = cnt[e];
+            ++slot_off;
+        }
+        pair_off += cnt[e];
+    }
+    if (shared && tid == 0) {
+        s_exp[tot_slots] = E;
+        s_pb[tot_slots] = 0;
+        s_pc[tot_slots] = n_tokens;
+    }
+    __syncthreads();
+    // 4) pairs (order inside a slot only picks an MFMA column)
+    for (int i = tid; i < n_assign; i += nt) {
+        const int t = i / top_k, k = i - t * top_k;
+        int pos = -1;
+        if (okv[i]) {
+            pos = atomicAdd(&cur[sid[i]], 1);
+            P.pair_token[pos] = t;
+            P.pair_weight[pos] = w[i];
+        }
+        P.token_pairs[(size_t)t * (top_k + 1) + k] = pos;
+    }
+    for (int t = tid; t < n_tokens; t += nt) {
+        if (shared) {
+            P.pair_token[t] = t;
+            P.pair_weight[t] = 1.0f;
+        }
+        P.token_pairs[(size_t)t * (top_k + 1) + top_k] = shared ? t : -1;
+    }
+    const int n_slots = tot_slots + (shared ? 1 : 0);
+    for (int sl = tid; sl < n_slots; sl += nt) {
+        P.slot_expert[sl] = s_exp[sl];
+        P.slot_pair_begin[sl] = s_pb[sl];
+        P.slot_pair_count[sl] = s_pc[sl];
+        const cx_expert_desc& e = tab[s_exp[sl]];
+        P.slot_rec[sl] = SlotRec{e.w_down, e.s_down, e.down_rb, 0};
+    }
+    // 5) items of <= item_cap pairs, routed first, shared last
+    const int schunk = (n_slots + nt - 1) / nt;
+    const int s0s = min(tid * schunk, n_slots), s1s = min(s0s + schunk, n_slots);
+    int my_items = 0;
+    for (int sl = s0s; sl < s1s; ++sl) my_items += (s_pc[sl] + item_cap - 1) / item_cap;
+    int tot_items = 0;
+    // (the scan's barriers also complete this block's pair_token writes)
+    int it = block_excl_scan(my_items, scan, &tot_items);
+    for (int sl = s0s; sl < s1s; ++sl) {
+        const int pb = s_pb[sl], pc = s_pc[sl];
+        const cx_expert_desc& e = tab[s_exp[sl]];
+        for (int o = 0; o < pc; o += item_cap) {
+            if (it < max_items) {
+                const int np = min(item_cap, pc - o), q0 = pb + o;
+                P.item_slot[it] = sl;
+                P.item_pair_begin[it] = q0;
+                P.item_pair_count[it] = np;
+                const int t0 = P.pair_token[q0];
+                const int t1 = np > 1 ? P.pair_token[q0 + 1] : 0;
+                const int t2 = np > 2 ? P.pair_token[q0 + 2] : 0;
+                const int t3 = np > 3 ? P.pair_token[q0 + 3] : 0;
+                P.item_rec[it] = ItemRec{e.w_up, e.w_gate, e.w_down, e.s_up, e.s_gate, e.s_down,
+                                         q0, np, e.up_rb, e.gate_rb, e.down_rb, 0, {t0, t1, t2, t3}};
+            }
+            ++it;
+        }
+    }
+    if (tid == 0) {
+        const int shared_items = shared ? (n_tokens + item_cap - 1) / item_cap : 0;
+        if (tot_items > max_items) s_err |= kErrPlanOverflow;
+        P.hdr->n_slots = n_slots;
+        P.hdr->n_items = min(tot_items, max_items);
+        P.hdr->n_pairs = s0 + tot_pairs;
+        P.hdr->n_routed_slots = tot_slots;
+        P.hdr->n_routed_items = min(tot_items - shared_items, max_items);
+        if (s_err) atomicOr(err_flag, s_err);
+    }
+}
+
+__global__ __launch_bounds__(kPlanThreads) void k_plan_staged(const int32_t* __restrict__ ids,
+                                                              const float* __restrict__ w,
+                                                              int n_tokens, int top_k,
+                                                              const cx_expert_desc* table,
+                                                              int n_experts, int has_shared,
+                                                              int item_cap, int max_items,
+                                                              PlanPtrs P, int* err_flag) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char plds[];
+    plan_build_staged(ids, w, n_tokens, top_k, table, n_experts, has_shared, item_cap, max_items,
+                      P, err_flag, plds);
+}
+
 __global__ __launch_bounds__(kPlanThreads) void k_plan(const int32_t* __restrict__ ids,
                                                        const float* __restrict__ w, int n_tokens,
                                                        int top_k, const cx_expert_desc* table,
@@ -1035,7 +1201,7 @@ constexpr int kLgE = 16;       // experts per workgroup tile
 constexpr int kLgT = 32;       // tokens per workgroup tile (two MFMA column tiles)
 constexpr int kLgWaves = 8;    // K split
 constexpr int kLgRing = 4;     // chunks in flight per wave
-constexpr int kLgMinTokens = 32;
+constexpr int kLgMinTokens = 64;  // below: too few tiles to fill the GPU
 
 bool logits_mfma_ok(int n_tokens, int hidden) {
     return n_tokens >= kLgMinTokens && hidden % (kLgWaves * 32 * kLgRing) == 0;
@@ -1473,6 +1639,12 @@ hipError_t launch_plan(const int32_t* ids, const float* w, int n_tokens, int top
                        const cx_expert_desc* table, int n_experts, int has_shared, int item_cap,
                        int max_items, PlanPtrs plan, int* err_flag, hipStream_t s) {
     const int threads = n_tokens * top_k <= 512 ? 256 : kPlanThreads;
+    const size_t staged = plan_staged_lds(n_tokens * top_k, n_experts, threads);
+    if (staged <= 65536) {
+        cx_launch(k_plan_staged, dim3(1), dim3(threads), staged, s, ids, w, n_tokens, top_k,
+                  table, n_experts, has_shared, item_cap, max_items, plan, err_flag);
+        return hipGetLastError();
+    }
     const size_t lds = sizeof(int) * (2 * (size_t)n_experts + threads);
     cx_launch(k_plan, dim3(1), dim3(threads), lds, s, ids, w, n_tokens, top_k, table,
               n_experts, has_shared, item_cap, max_items, plan, err_flag);

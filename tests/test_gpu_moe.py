@@ -64,8 +64,8 @@ def test_router_vs_oracle(gpu, oracle, T, E, H, G, TG, K):
 def test_router_many_tokens_fp32_operands(gpu, oracle, xdt, wdt):
     """The fp64-MFMA logits path (T >= 32) with fp32 activations or weights:
     products of fp32 values are exact in fp64 too."""
-    print(f"[route] T=40 x={xdt} w={wdt}", flush=True)
-    T, E, H = 40, 64, 2048
+    print(f"[route] T=72 x={xdt} w={wdt}", flush=True)
+    T, E, H = 72, 64, 2048
     x, w, bias = _router_inputs(gpu, 300, T, E, H)
     x = (x.float() * 1.37).to(xdt)   # fp32 values with more than 8 significant bits
     w = (w.float() * 0.73).to(wdt)
@@ -196,8 +196,9 @@ def test_moe_layer_fused_router(gpu, oracle):
         _free(layer, experts, sh)
 
 
-def test_moe_bad_and_missing_experts_reported(gpu):
-    print("[moe] error flags", flush=True)
+@pytest.mark.parametrize("prefill", [False, True])
+def test_moe_bad_and_missing_experts_reported(gpu, prefill):
+    print(f"[moe] error flags prefill={prefill}", flush=True)
     from constellation_amd import CxError
     from constellation_amd.engine import Expert, Layer
     H, I = 1024, 512
@@ -207,7 +208,7 @@ def test_moe_bad_and_missing_experts_reported(gpu):
         x = gpu.gen_normal(1, 1, (2, H), 1.0, torch.bfloat16)
         ids = torch.tensor([[0, 7], [0, 2]], dtype=torch.int32, device="cuda")
         w = torch.ones((2, 2), dtype=torch.float32, device="cuda")
-        gpu.moe(layer, x, ids, w)
+        gpu.moe(layer, x, ids, w, prefill=prefill)
         with pytest.raises(CxError):
             gpu.sync()
         gpu.sync()  # flag cleared
