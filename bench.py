@@ -52,6 +52,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-extra-configs", action="store_true",
                     help="skip the single-expert, prefill and node-share measurements")
+    ap.add_argument("--extras", default="0,3,4",
+                    help="comma list of the extra configs to measure: 0 single expert, "
+                         "3 prefill chunk, 4 node share (default: all)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="first run a plain device copy of this many MiB (three times): the "
                          "known-size kernel that scales HBM counters of a --pmc profile")
@@ -398,15 +401,17 @@ def main() -> int:
                          "layer_gbs": layer_bytes(16, u16) / (ms16 * 1e-3) / 1e9,
                          "layer_frac_of_8tbs": layer_bytes(16, u16) / (ms16 * 1e-3) / 1e9 / HBM_PEAK_GBS,
                          "kernels": prof16}
-    if not args.no_extra_configs:
+    want = set() if args.no_extra_configs else {c.strip() for c in args.extras.split(",") if c.strip()}
+    if "0" in want:
         extras["config0_single_expert"] = bench_single_expert(ctx, layers, max(100, args.steps // 2))
+    if "3" in want:
         extras["config3_prefill"] = bench_prefill(ctx, layers, 10)
     for L in layers:  # release the rotated layers before the node-share residency
         L["layer"].close()
         for e in L["experts"] + [L["shared"]]:
             e.free()
     layers = None
-    if not args.no_extra_configs:
+    if "4" in want:
         extras["config4_node_share"] = bench_node_share(ctx, 5)
     gu = prof1["gate_up"]
     gu_bytes = gate_up_bytes(1, u1)

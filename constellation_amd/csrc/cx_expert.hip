@@ -454,12 +454,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 
 // ---------------------------------------------------------------------------
 // Grouped GEMM for items of up to 64 pairs (cx_grouped.h): gate/up over
-// grid = (inter/64, items), down over grid = (hidden/256, items).  LDS rings
+// inter/64 row tiles x items as a one-dimensional XCD-aware grid
+// (xcd_tile_item: an item's x rows stay in one L2), down over grid =
+// (hidden/256, items) (measured: the XCD mapping does not help it).  LDS rings
 // of 80 KB / 128 KB: two gate/up or one down workgroup per CU.
 template <int NKB, bool F16, bool SINGLE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_gu_grp(ExpertLaunch L) {
     extern __shared__ __attribute__((aligned(16))) unsigned char grp_lds[];
-    grp_gate_up_tile<NKB, F16, SINGLE>(L, blockIdx.x, blockIdx.y, grp_lds);
+    int tile, item;
+    xcd_tile_item(blockIdx.x, L.inter / kGuGrpRows, &tile, &item);
+    grp_gate_up_tile<NKB, F16, SINGLE>(L, tile, item, grp_lds);
 }
 
 template <int NKB, bool SINGLE>
@@ -698,7 +702,7 @@ void go_gu_grp(const ExpertLaunch& L, dim3 grid, hipStream_t s) {
 }
 
 bool pick_gu_grp(const ExpertLaunch& L, int items, hipStream_t s) {
-    const dim3 grid(L.inter / kGuGrpRows, items);
+    const dim3 grid(xcd_grid(L.inter / kGuGrpRows, items));
     const bool f16 = L.in_dtype == CX_DTYPE_FP16;
     switch (L.hidden / kKB) {
         case 56: f16 ? go_gu_grp<56, true>(L, grid, s) : go_gu_grp<56, false>(L, grid, s); return true;

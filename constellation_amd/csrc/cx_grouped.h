@@ -51,6 +51,22 @@ __device__ __forceinline__ void lds_write_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// XCD-aware placement of a (row tile, item) grid launched as one dimension
+// of n_tiles * round_up(items, 8) workgroups.  Workgroups are dealt to the 8
+// XCDs round-robin, so linear id w runs on XCD w % 8.  Every row tile of one
+// item is mapped to the same XCD (item = 8 * (j / n_tiles) + w % 8,
+// tile = j % n_tiles with j = w / 8), so the item's activation rows are
+// fetched into that XCD's L2 only, and reused there by all its tiles.
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ void xcd_tile_item(int w, int n_tiles, int* tile, int* item) {
+    const int j = w / kXcds;
+    *tile = j % n_tiles;
+    *item = (j / n_tiles) * kXcds + (w % kXcds);
+}
+
+inline int xcd_grid(int n_tiles, int items) { return n_tiles * ((items + kXcds - 1) / kXcds) * kXcds; }
+
 // Scale of k-block k of the lane-distributed scale row `v` (lane l holds
 // k-block l).
 __device__ __forceinline__ float lane_scale(float v, int k) {
