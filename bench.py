@@ -52,8 +52,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-extra-configs", action="store_true",
                     help="skip the single-expert, prefill and node-share measurements")
-    ap.add_argument("--extras", default="0,3,4",
-                    help="comma list of the extra configs to measure: 0 single expert, "
+    ap.add_argument("--extras", default="h,0,3,4",
+                    help="comma list of the extra measurements: h host boundary at B=1 "
+                         "(layer request vs per-expert requests), 0 single expert, "
                          "3 prefill chunk, 4 node share (default: all)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="first run a plain device copy of this many MiB (three times): the "
@@ -211,6 +212,50 @@ def bench_single_expert(ctx, layers, steps):
             "host_buffer_us_per_request": host_us,
             "host_buffer_note": "cx_expert_run_host, fp16 in/out, wall clock incl. pinned "
                                 "H2D/D2H and stream sync (PCIe-inclusive)"}
+
+
+def bench_host_boundary(ctx, layers, pool, n):
+    """The node boundary at B=1, host buffers in and out (PCIe-inclusive wall
+    clock, never `value`): one MoeLayerRequest body (routes + activation in,
+    combined partial sum out; cx_moe_layer_request_run) against the
+    reference's pattern of one InferRequest per selected expert plus the
+    shared expert, run back to back (cx_expert_run_host, 9 calls)."""
+    import numpy as np
+    import torch
+    from constellation_amd import BF16
+    from constellation_amd import moe_layer_protocol as P
+    bodies, routes = [], []
+    for i in range(16):
+        L = layers[i % len(layers)]
+        x = pool[i:i + 1]
+        ids, w = ctx.route(x, L["w_r"], L["bias"], n_group=NGROUP, topk_group=TOPK_GROUP,
+                           top_k=TOPK, routed_scaling_factor=SCALE)
+        ids, w = ids.cpu().numpy(), w.cpu().numpy()
+        xb = x.cpu().view(torch.int16).numpy().tobytes()
+        bodies.append(P.encode_moe_layer_request({
+            "layer_id": i % len(layers), "batch_size": 1, "hidden_dim": H, "top_k": TOPK,
+            "input_dtype": BF16, "output_dtype": BF16, "flags": P.FLAG_SHARED,
+            "expert_ids": ids, "expert_weights": w, "activation": xb}))
+        routes.append((L, ids[0], xb))
+    for i in range(8):
+        ctx.moe_layer_request(layers[i % len(layers)]["layer"], bodies[i])
+    t0 = time.perf_counter()
+    for i in range(n):
+        r = P.decode_moe_layer_response(ctx.moe_layer_request(layers[i % 16 % len(layers)]["layer"],
+                                                              bodies[i % 16]))
+        assert r["status_code"] == 0
+    layer_us = (time.perf_counter() - t0) / n * 1e6
+    t0 = time.perf_counter()
+    for i in range(n):
+        L, ids, xb = routes[i % 16]
+        for e in ids:
+            ctx.expert_run_host(L["experts"][int(e)], xb, BF16, 1, BF16)
+        ctx.expert_run_host(L["shared"], xb, BF16, 1, BF16)
+    per_expert_us = (time.perf_counter() - t0) / n * 1e6
+    return {"layer_request_us": layer_us, "per_expert_requests_us": per_expert_us,
+            "note": "B=1, host bytes in and out, wall clock incl. pinned H2D/D2H and stream "
+                    "sync; layer request = one MoeLayerRequest body (8 routes + shared) vs 9 "
+                    "sequential single-expert host requests as the reference's dispatch"}
 
 
 def bench_prefill(ctx, layers, steps):
@@ -402,6 +447,8 @@ def main() -> int:
                          "layer_frac_of_8tbs": layer_bytes(16, u16) / (ms16 * 1e-3) / 1e9 / HBM_PEAK_GBS,
                          "kernels": prof16}
     want = set() if args.no_extra_configs else {c.strip() for c in args.extras.split(",") if c.strip()}
+    if "h" in want:
+        extras["b1"]["host_boundary"] = bench_host_boundary(ctx, layers, pool, 100)
     if "0" in want:
         extras["config0_single_expert"] = bench_single_expert(ctx, layers, max(100, args.steps // 2))
     if "3" in want:

@@ -41,6 +41,15 @@ class ExpertDesc(C.Structure):
     ]
 
 
+class MoeLayerRequestInfo(C.Structure):
+    """cx_moe_layer_request_info: header fields of a MoeLayerRequest body."""
+    _fields_ = [
+        ("layer_id", C.c_int32), ("batch_size", C.c_int32), ("hidden_dim", C.c_int32),
+        ("top_k", C.c_int32), ("input_dtype", C.c_uint32), ("output_dtype", C.c_uint32),
+        ("flags", C.c_uint32),
+    ]
+
+
 class DeviceInfo(C.Structure):
     _fields_ = [
         ("name", C.c_char * 128), ("arch", C.c_char * 64),
@@ -79,6 +88,10 @@ _SIGS = {
     "cx_moe_prefill": (_I, [_P, _P, _P, _I, _I, _P, _P, _I, _P, _I, _P, _P]),
     "cx_moe_layer": (_I, [_P, _P, _P, _I, _I, _P, _I, _P, _P, _I, _I, _I, _I, C.c_float,
                           _P, _I, _P, _P, _P, _P]),
+    "cx_moe_layer_request_peek": (_I, [_P, C.c_size_t, C.POINTER(MoeLayerRequestInfo)]),
+    "cx_moe_layer_response_size": (C.c_size_t, [_I, _I]),
+    "cx_moe_layer_request_run": (_I, [_P, _P, _P, C.c_size_t, _P, C.c_size_t,
+                                      C.POINTER(C.c_size_t)]),
     "cx_gen_fp8_matrix": (_I, [_P, C.c_uint64, C.c_uint64, _I, _I, _I, _I, C.c_float, _P, _P,
                                _P]),
     "cx_gen_normal": (_I, [_P, C.c_uint64, C.c_uint64, C.c_uint64, C.c_float, _I, _P, _P]),

@@ -5,10 +5,14 @@
 #pragma once
 
 #include <memory>
+#include <string>
+#include <unordered_map>
+#include <vector>
 
 #include "expert_node_v2/backend/backend_workspace_v2.h"
 
 struct cx_ctx;
+struct cx_layer;
 
 namespace expert_node_v2 {
 
@@ -25,11 +29,36 @@ public:
                           const common::InferRequestMsg& req,
                           common::InferResponseMsg* resp) override;
 
+    // Whole-layer request (MoeLayerRequest, msg_type 42; no counterpart in
+    // the reference's v1 protocol): layer_experts[i] is the device storage of
+    // the layer's local expert i on this worker (nullptr: not resident here),
+    // shared the layer's shared expert (nullable).  Fills resp_body with the
+    // MoeLayerResponse body; request-level failures are status codes in it
+    // (1 unknown expert, 2 not resident, 4 execution failure, as
+    // worker.cc:113-132).  Returns false only for a body that does not decode.
+    // The device expert table of a layer is built once and reused while its
+    // storages stay the same.
+    bool RunMoeLayerRequest(int layer_id,
+                            const std::vector<const ExpertDeviceStorageV2*>& layer_experts,
+                            const ExpertDeviceStorageV2* shared, const std::string& req_body,
+                            std::string* resp_body);
+
     bool ok() const { return ctx_ != nullptr; }
 
 private:
+    // Cached device table of one layer, keyed by the descriptors it was
+    // built from (device pointers and blocks, so a re-uploaded expert at the
+    // same storage address still invalidates it).
+    struct LayerTable {
+        std::vector<unsigned char> key;
+        cx_layer* layer = nullptr;
+    };
+    cx_layer* layer_for(int layer_id, const std::vector<const ExpertDeviceStorageV2*>& experts,
+                        const ExpertDeviceStorageV2* shared);
+
     int local_gpu_id_ = -1;
     cx_ctx* ctx_ = nullptr;
+    std::unordered_map<int, LayerTable> layers_;
 };
 
 }  // namespace expert_node_v2

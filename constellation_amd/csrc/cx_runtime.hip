@@ -221,6 +221,7 @@ struct cx_layer {
     int hidden = 0, inter = 0;
     cx_expert_desc* table = nullptr;   // device [n_experts + 1], entry n_experts = shared
     cx_expert_desc shared_desc{};      // host copy of the shared expert (when has_shared)
+    std::vector<uint8_t> resident;     // host copy: entry i holds an expert
 };
 
 namespace {
@@ -559,6 +560,93 @@ int fill_route(cx_ctx* ctx, const void* x, int x_dtype, const void* w_router, in
 }  // namespace
 
 // ===========================================================================
+// Whole-layer wire message helpers (MoeLayerRequest / MoeLayerResponse, cx_moe.h).
+namespace {
+
+struct LayerReq {
+    cx_moe_layer_request_info info;
+    const uint8_t* ids;  // int32 [n_routes], little-endian, unaligned
+    const uint8_t* w;    // float [n_routes]
+    const uint8_t* act;  // [T, H] 16-bit
+    size_t n_routes, act_bytes;
+};
+
+bool rd32(const uint8_t* b, size_t n, size_t* off, uint32_t* v) {
+    if (*off > n || n - *off < 4) return false;
+    std::memcpy(v, b + *off, 4);
+    *off += 4;
+    return true;
+}
+
+// Exact-length decode (every field consumed, nothing trailing), as
+// DecodeInferRequestBody (common/infer_codec.cc:22-43) requires.
+int parse_layer_req(const uint8_t* body, size_t len, LayerReq* r) {
+    if (!body) return fail(CX_EINVAL, "NULL request body");
+    size_t off = 0;
+    uint32_t f[8];
+    for (int i = 0; i < 8; ++i)
+        if (!rd32(body, len, &off, &f[i])) return fail(CX_EINVAL, "request body truncated in header");
+    cx_moe_layer_request_info& h = r->info;
+    h.layer_id = (int32_t)f[0];
+    h.batch_size = (int32_t)f[1];
+    h.hidden_dim = (int32_t)f[2];
+    h.top_k = (int32_t)f[3];
+    h.input_dtype = f[4];
+    h.output_dtype = f[5];
+    h.flags = f[6];
+    const uint32_t n_routes = f[7];
+    if (h.batch_size <= 0 || h.hidden_dim <= 0 || h.top_k < 0 || h.top_k > 64)
+        return fail(CX_EINVAL, "bad batch_size/hidden_dim/top_k (%d, %d, %d)", h.batch_size,
+                    h.hidden_dim, h.top_k);
+    if (!act16((int)h.input_dtype) || !act16((int)h.output_dtype))
+        return fail(CX_EINVAL, "activation dtypes must be fp16 (1) or bf16 (2)");
+    if (h.flags & ~CX_MOE_LAYER_FLAG_SHARED) return fail(CX_EINVAL, "unknown flags 0x%x", h.flags);
+    if ((uint64_t)n_routes != (uint64_t)h.batch_size * (uint64_t)h.top_k)
+        return fail(CX_EINVAL, "n_routes %u != batch_size * top_k", n_routes);
+    const uint64_t rb = (uint64_t)n_routes * 4;
+    if (len - off < 2 * rb) return fail(CX_EINVAL, "request body truncated in routes");
+    r->n_routes = n_routes;
+    r->ids = body + off;
+    r->w = body + off + rb;
+    off += 2 * rb;
+    uint32_t nb = 0;
+    if (!rd32(body, len, &off, &nb)) return fail(CX_EINVAL, "request body truncated before activation");
+    const uint64_t want = (uint64_t)h.batch_size * (uint64_t)h.hidden_dim * 2;
+    if (nb != want) return fail(CX_EINVAL, "activation_nbytes %u != batch*hidden*2", nb);
+    if (len - off != nb) return fail(CX_EINVAL, "request body length mismatch (trailing or missing bytes)");
+    r->act = body + off;
+    r->act_bytes = nb;
+    return CX_OK;
+}
+
+size_t put32(uint8_t* b, size_t off, uint32_t v) {
+    std::memcpy(b + off, &v, 4);
+    return off + 4;
+}
+
+size_t write_layer_resp(uint8_t* resp, int status, const cx_moe_layer_request_info& h,
+                        uint32_t nbytes) {
+    size_t o = 0;
+    o = put32(resp, o, (uint32_t)status);
+    o = put32(resp, o, (uint32_t)h.batch_size);
+    o = put32(resp, o, (uint32_t)h.hidden_dim);
+    o = put32(resp, o, h.output_dtype);
+    o = put32(resp, o, nbytes);
+    return o + nbytes;  // body length: header + the output bytes that follow it
+}
+
+int pin_ensure(void** p, size_t* cap, size_t bytes) {
+    if (*cap >= bytes) return CX_OK;
+    if (*p) (void)hipHostFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    CX_HIP(hipHostMalloc(p, bytes, hipHostMallocDefault));
+    *cap = bytes;
+    return CX_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* cx_last_error(void) { return g_err.c_str(); }
@@ -853,6 +941,8 @@ int cx_layer_create(cx_ctx* ctx, int n_experts, const cx_expert_desc* const* exp
     if (!L) return fail(CX_ENOMEM, "out of host memory");
     L->n_experts = n_experts;
     L->has_shared = shared ? 1 : 0;
+    L->resident.assign(n_experts, 0);
+    for (int i = 0; i < n_experts; ++i) L->resident[i] = (experts && experts[i]) ? 1 : 0;
     L->shared_desc = host[n_experts];
     L->fast = fast;
     L->hidden = H;
@@ -934,6 +1024,99 @@ int cx_moe_layer(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype
         return rc;
     return moe_run(ctx, layer, x, in_dtype, n_tokens, ids, w, top_k, y, out_dtype, y_f32, s,
                    n_tokens > kTileTok, &R);
+}
+
+// ---------------------------------------------------------------------------
+// Whole-layer wire message (MoeLayerRequest / MoeLayerResponse, cx_moe.h).
+
+
+int cx_moe_layer_request_peek(const uint8_t* body, size_t body_len, cx_moe_layer_request_info* out) {
+    if (!out) return fail(CX_EINVAL, "NULL output");
+    LayerReq r;
+    const int rc = parse_layer_req(body, body_len, &r);
+    if (rc) return rc;
+    *out = r.info;
+    return CX_OK;
+}
+
+size_t cx_moe_layer_response_size(int batch_size, int hidden_dim) {
+    if (batch_size <= 0 || hidden_dim <= 0) return 20;
+    return 20 + (size_t)batch_size * (size_t)hidden_dim * 2;
+}
+
+int cx_moe_layer_request_run(cx_ctx* ctx, const cx_layer* layer, const uint8_t* body,
+                             size_t body_len, uint8_t* resp, size_t resp_cap, size_t* resp_len) {
+    if (!ctx || !layer || !resp || !resp_len) return fail(CX_EINVAL, "NULL argument");
+    *resp_len = 0;
+    LayerReq r;
+    int rc = parse_layer_req(body, body_len, &r);
+    if (rc) return rc;
+    const cx_moe_layer_request_info& h = r.info;
+    const int T = h.batch_size, H = h.hidden_dim, K = h.top_k;
+    const size_t out_bytes = (size_t)T * H * 2;
+    if (resp_cap < 20 + out_bytes) return fail(CX_EINVAL, "response buffer %zu < %zu", resp_cap, 20 + out_bytes);
+    // request-level checks, mapped to the worker's status codes
+    int status = 0;
+    bool any_route = false;
+    for (size_t i = 0; i < r.n_routes && status != 1; ++i) {
+        int32_t id;
+        std::memcpy(&id, r.ids + 4 * i, 4);
+        if (id < 0) continue;
+        any_route = true;
+        if (id >= layer->n_experts) status = 1;
+        else if (!layer->resident[id] && status == 0) status = 2;
+    }
+    const bool want_shared = (h.flags & CX_MOE_LAYER_FLAG_SHARED) != 0;
+    if (status == 0 && want_shared && !layer->has_shared) status = 2;
+    if (status == 0 && (H != layer->hidden || !layer->fast)) status = 4;
+    if (status != 0) {
+        *resp_len = write_layer_resp(resp, status, h, 0);
+        return CX_OK;
+    }
+    if ((rc = set_device(ctx->device))) return rc;
+    hipStream_t s = ctx->own_stream;
+    if (!any_route && !want_shared) {  // nothing on this node: y = 0
+        std::memset(resp + 20, 0, out_bytes);
+        *resp_len = write_layer_resp(resp, 0, h, (uint32_t)out_bytes);
+        return CX_OK;
+    }
+    // staging: [ids | weights | pad | activation], one copy each way
+    const size_t rb = r.n_routes * 4;
+    const size_t act_off = (2 * rb + 255) & ~(size_t)255;
+    const size_t in_bytes = act_off + r.act_bytes;
+    if ((rc = pin_ensure(&ctx->pin_x, &ctx->pin_x_bytes, in_bytes))) return rc;
+    if ((rc = pin_ensure(&ctx->pin_y, &ctx->pin_y_bytes, out_bytes))) return rc;
+    if ((rc = ensure(&ctx->dx, in_bytes, s))) return rc;
+    if ((rc = ensure(&ctx->dy, out_bytes, s))) return rc;
+    uint8_t* px = static_cast<uint8_t*>(ctx->pin_x);
+    std::memcpy(px, r.ids, 2 * rb);
+    std::memcpy(px + act_off, r.act, r.act_bytes);
+    CX_HIP(hipMemcpyAsync(ctx->dx.p, px, in_bytes, hipMemcpyHostToDevice, s));
+    uint8_t* dx = static_cast<uint8_t*>(ctx->dx.p);
+    cx_layer view = *layer;  // the shared expert joins only when asked for
+    view.has_shared = want_shared ? layer->has_shared : 0;
+    rc = moe_run(ctx, &view, dx + act_off, (int)h.input_dtype, T,
+                 K > 0 ? reinterpret_cast<const int32_t*>(dx) : nullptr,
+                 K > 0 ? reinterpret_cast<const float*>(dx + rb) : nullptr, K, ctx->dy.p,
+                 (int)h.output_dtype, nullptr, s, T > kTileTok, nullptr);
+    if (rc) {
+        (void)hipStreamSynchronize(s);
+        *resp_len = write_layer_resp(resp, 4, h, 0);
+        return CX_OK;
+    }
+    CX_HIP(hipMemcpyAsync(ctx->pin_y, ctx->dy.p, out_bytes, hipMemcpyDeviceToHost, s));
+    int flag = 0;
+    CX_HIP(hipMemcpyAsync(&flag, ctx->err_flag, sizeof(int), hipMemcpyDeviceToHost, s));
+    CX_HIP(hipStreamSynchronize(s));
+    if (flag != 0) {  // a device check failed (e.g. a route listed twice for one token)
+        CX_HIP(hipMemsetAsync(ctx->err_flag, 0, sizeof(int), s));
+        CX_HIP(hipStreamSynchronize(s));
+        *resp_len = write_layer_resp(resp, 4, h, 0);
+        return CX_OK;
+    }
+    std::memcpy(resp + 20, ctx->pin_y, out_bytes);
+    *resp_len = write_layer_resp(resp, 0, h, (uint32_t)out_bytes);
+    return CX_OK;
 }
 
 int cx_gen_fp8_matrix(cx_ctx* ctx, uint64_t seed, uint64_t stream_id, int rows, int cols,

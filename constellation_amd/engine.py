@@ -12,7 +12,8 @@ from typing import Optional, Sequence
 import numpy as np
 import torch
 
-from ._lib import BF16, F32, FP16, CxError, DeviceInfo, ExpertDesc, check, lib
+from ._lib import (BF16, F32, FP16, CxError, DeviceInfo, ExpertDesc, MoeLayerRequestInfo, check,
+                   lib)
 
 _TORCH_TO_CX = {torch.float16: FP16, torch.bfloat16: BF16, torch.float32: F32}
 _CX_TO_TORCH = {FP16: torch.float16, BF16: torch.bfloat16, F32: torch.float32}
@@ -258,6 +259,20 @@ class Context:
         check(fn(self.handle, layer.handle, x.data_ptr(), cx_dtype(x.dtype), T, ids.data_ptr(),
                  w.data_ptr(), K, y.data_ptr(), cx_dtype(out_dtype), _ptr(yf), self.stream()))
         return (y, yf) if want_f32 else y
+
+    # -- whole-layer wire message (MoeLayerRequest / MoeLayerResponse) -------------
+    def moe_layer_request(self, layer: Layer, body: bytes) -> bytes:
+        """Runs one MoeLayerRequest body (host bytes, moe_layer_protocol) on
+        `layer` and returns the MoeLayerResponse body (host bytes)."""
+        info = MoeLayerRequestInfo()
+        b = np.frombuffer(body, np.uint8)
+        check(lib().cx_moe_layer_request_peek(b.ctypes.data, b.size, C.byref(info)))
+        cap = lib().cx_moe_layer_response_size(info.batch_size, info.hidden_dim)
+        out = np.empty(cap, np.uint8)
+        n = C.c_size_t(0)
+        check(lib().cx_moe_layer_request_run(self.handle, layer.handle, b.ctypes.data, b.size,
+                                             out.ctypes.data, out.size, C.byref(n)))
+        return out[:n.value].tobytes()
 
     def moe_layer(self, layer: Layer, x: torch.Tensor, w_router: torch.Tensor, bias: torch.Tensor, *,
                   resident: Optional[torch.Tensor] = None, n_group: int = 8, topk_group: int = 4,

@@ -214,6 +214,55 @@ CX_API int cx_moe_layer(cx_ctx* ctx, const cx_layer* layer,
                  void* y, int out_dtype, float* y_f32,
                  int32_t* topk_ids, float* topk_w, void* stream);
 
+/* ---- whole-layer wire message ---------------------------------------------
+ * MoeLayerRequest (msg_type 42) / MoeLayerResponse (43): one request per
+ * node per layer instead of one InferRequest per selected expert, sent
+ * sequentially (moe_layer_runtime.py:111-145, infer_one_expert :27-81).  No
+ * counterpart in the reference's v1 protocol (common/protocol.h:13-37); the
+ * types are additive and v1 InferRequest/InferResponse stay byte-identical.
+ * Little-endian bodies in the style of common/infer_codec.cc:7-76:
+ *   request:  i32 layer_id, i32 batch_size T, i32 hidden_dim H, i32 top_k K,
+ *             u32 input_dtype, u32 output_dtype (ActivationDType: 1 fp16,
+ *             2 bf16), u32 flags (bit 0: add the layer's shared expert),
+ *             u32 n_routes (= T*K), i32 expert_ids[n_routes] (local ids of the
+ *             layer, -1 = no expert on this node), f32 expert_weights[n_routes],
+ *             u32 activation_nbytes (= T*H*2), activation bytes [T, H].
+ *   response: i32 status_code (0 ok, 1 expert unknown, 2 expert not resident,
+ *             4 execution failure: the codes of worker.cc:113-132),
+ *             i32 batch_size, i32 hidden_dim, u32 output_dtype,
+ *             u32 output_nbytes (T*H*2, or 0 on failure), output bytes [T, H]:
+ *             y[t] = sum_k w[t][k] * expert_k(x[t]) in route order, then
+ *             + shared(x[t]) (combine_outputs_torch, moe_layer_runtime.py:
+ *             148-167, and full_model_runtime.py:348), in fp32, rounded once. */
+#define CX_MSG_MOE_LAYER_REQUEST 42
+#define CX_MSG_MOE_LAYER_RESPONSE 43
+#define CX_MOE_LAYER_FLAG_SHARED 1u
+
+typedef struct cx_moe_layer_request_info {
+    int32_t layer_id, batch_size, hidden_dim, top_k;
+    uint32_t input_dtype, output_dtype, flags;
+} cx_moe_layer_request_info;
+
+/* Validates a request body (exact length, field ranges) and returns its
+ * header fields, so a worker can pick the layer before running it.  Host
+ * only. */
+CX_API int cx_moe_layer_request_peek(const uint8_t* body, size_t body_len,
+                              cx_moe_layer_request_info* out);
+/* Bytes of a full (status 0) response body for T tokens of hidden H. */
+CX_API size_t cx_moe_layer_response_size(int batch_size, int hidden_dim);
+/* Runs one request body against `layer` (whose entry i is the layer's local
+ * expert i on this node) through persistent pinned and device buffers: one
+ * host->device copy of routes + activation, cx_moe_decode (T <= 16) or
+ * cx_moe_prefill, one device->host copy.  Writes the response body into
+ * resp[resp_cap] (resp_cap >= cx_moe_layer_response_size) and its length
+ * into *resp_len.  Request-level failures (unknown / non-resident expert,
+ * hidden mismatch, a device check) become a status code in the response
+ * and CX_OK; a malformed body or an undersized buffer returns CX_EINVAL
+ * without a response. */
+CX_API int cx_moe_layer_request_run(cx_ctx* ctx, const cx_layer* layer,
+                             const uint8_t* body, size_t body_len,
+                             uint8_t* resp, size_t resp_cap, size_t* resp_len);
+
 /* ---- synthetic data ------------------------------------------------------
  * Counter-based generator shared bit-for-bit with the CPU oracle, so any
  * single tensor can be regenerated on either side:

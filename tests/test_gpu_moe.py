@@ -405,3 +405,75 @@ def test_full_size_prefill_grouped_items(gpu, oracle):
         assert np.array_equal(_bits(y)[sel], oracle.encode_act(yf, BF16, "rne"))
     finally:
         _free(layer, experts, sh)
+
+
+@pytest.mark.parametrize("T,dtype,shared", [(1, torch.bfloat16, True), (5, torch.float16, True),
+                                             (20, torch.bfloat16, True), (3, torch.bfloat16, False)])
+def test_moe_layer_request_end_to_end(gpu, oracle, T, dtype, shared):
+    """One MoeLayerRequest body in, one MoeLayerResponse body out (host bytes,
+    pinned staging): equal bit for bit to the device-pointer path on the same
+    routes, and within the parity bound of the oracle's combine."""
+    from constellation_amd import moe_layer_protocol as P
+    print(f"[moe] layer request T={T} {dtype} shared={shared}", flush=True)
+    E, H, I, K = 16, 1024, 512, 4
+    layer, experts, sh, cpu, cpu_sh = _make_layer(gpu, oracle, E, H, I, seed=101 + T)
+    try:
+        x = gpu.gen_normal(102 + T, 1, (T, H), 1.0, dtype)
+        rng = np.random.default_rng(T)
+        ids = np.stack([rng.choice(E, K, replace=False) for _ in range(T)]).astype(np.int32)
+        ids[0, K - 1] = -1  # a route served by another node
+        wts = rng.uniform(0.05, 1.0, ids.shape).astype(np.float32)
+        enc = FP16 if dtype == torch.float16 else BF16
+        body = P.encode_moe_layer_request({
+            "layer_id": 3, "batch_size": T, "hidden_dim": H, "top_k": K, "input_dtype": enc,
+            "output_dtype": enc, "flags": P.FLAG_SHARED if shared else 0, "expert_ids": ids,
+            "expert_weights": wts, "activation": x.cpu().view(torch.int16).numpy().tobytes()})
+        resp = P.decode_moe_layer_response(gpu.moe_layer_request(layer, body))
+        assert resp["status_code"] == 0 and resp["batch_size"] == T and resp["hidden_dim"] == H
+        got = np.frombuffer(resp["output"], np.uint16).reshape(T, H)
+        if shared:  # the device-pointer path adds the layer's shared expert too
+            y = gpu.moe(layer, x, torch.from_numpy(ids).cuda(), torch.from_numpy(wts).cuda(),
+                        prefill=T > 16)
+            gpu.sync()
+            assert np.array_equal(got, _bits(y))
+        ref = _oracle_moe(oracle, cpu, cpu_sh if shared else None, x.float().cpu().numpy(), ids, wts)
+        yv = oracle.decode_act(got.reshape(-1), enc).reshape(T, H)
+        assert rel_l2(yv, ref) < 1e-2 and np.abs(yv - ref).max() < 2e-2
+    finally:
+        _free(layer, experts, sh)
+
+
+def test_moe_layer_request_status_codes(gpu, oracle):
+    """worker.cc:113-132 codes: 1 unknown expert, 2 not resident (also the
+    shared expert asked of a layer without one), 4 execution failure (a
+    route listed twice); failures carry no output."""
+    from constellation_amd import moe_layer_protocol as P
+    from constellation_amd.engine import Expert, Layer
+    print("[moe] layer request status codes", flush=True)
+    H, I = 1024, 512
+    e0 = Expert.generate(0, 1, 0x10, hidden=H, inter=I)
+    layer = Layer(gpu, [e0, None, None, None])
+    try:
+        x = gpu.gen_normal(1, 1, (2, H), 1.0, torch.bfloat16)
+        act = x.cpu().view(torch.int16).numpy().tobytes()
+
+        def run(ids, flags=0):
+            ids = np.asarray(ids, np.int32)
+            body = P.encode_moe_layer_request({
+                "layer_id": 0, "batch_size": 2, "hidden_dim": H, "top_k": ids.shape[1],
+                "input_dtype": BF16, "output_dtype": BF16, "flags": flags, "expert_ids": ids,
+                "expert_weights": np.full(ids.shape, 0.5, np.float32), "activation": act})
+            return P.decode_moe_layer_response(gpu.moe_layer_request(layer, body))
+
+        ok = run([[0, -1], [0, -1]])
+        assert ok["status_code"] == 0 and len(ok["output"]) == 2 * H * 2
+        for ids, flags, code in (([[0, 7], [0, -1]], 0, 1), ([[0, 2], [0, -1]], 0, 2),
+                                 ([[0, -1], [0, -1]], P.FLAG_SHARED, 2), ([[0, 0], [0, -1]], 0, 4)):
+            r = run(ids, flags)
+            assert r["status_code"] == code and r["output"] == b"", (ids, flags, r["status_code"])
+        again = run([[0, -1], [0, -1]])  # a failure leaves the context usable
+        assert again == ok
+    finally:
+        torch.cuda.synchronize()
+        layer.close()
+        e0.free()
