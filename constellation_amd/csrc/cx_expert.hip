@@ -27,7 +27,6 @@
 //  * The k order inside a k-block is permuted identically for the weight
 //    (A) and activation (B) operands, so any lane->k assignment of the MFMA
 //    is valid; loads stay contiguous.
-#include <cstdlib>
 
 #include "cx_down.h"
 #include "cx_gate_up.h"
@@ -627,11 +626,6 @@ bool fast_path_ok(const cx_expert_desc& e) {
 }
 
 namespace {
-
-int env_int(const char* name, int dflt) {
-    const char* v = std::getenv(name);
-    return v ? std::atoi(v) : dflt;
-}
 
 template <int NKB, int KS, int MAXT, bool F16>
 void go_gate_up(const ExpertLaunch& L, dim3 grid, hipStream_t s) {
