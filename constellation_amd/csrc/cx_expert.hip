@@ -324,9 +324,15 @@ __global__ __launch_bounds__(256) void k_down_rt(ExpertLaunch L) {
 // ---------------------------------------------------------------------------
 // Phase A with a compile-time trip count: gate_up_tile (cx_gate_up.h) over
 // grid = (inter/16, items).
+// With L.gu_part set (decode, grouped mode), the last row of the grid
+// finalises the shared expert's h from its stage-2 k-part sums.
 template <int NKB, int D, int MAXT, bool F16, bool XLDS, int KS, bool SINGLE>
 __global__ __launch_bounds__(64 * KS) void k_gate_up_t(ExpertLaunch L) {
     extern __shared__ __attribute__((aligned(16))) unsigned char gu_lds[];
+    if (!SINGLE && MAXT == 1 && L.gu_part != nullptr && blockIdx.y == gridDim.y - 1) {
+        shared_h_finalize(L, blockIdx.x);
+        return;
+    }
     gate_up_tile<NKB, D, MAXT, F16, XLDS, KS, SINGLE>(L, blockIdx.x, blockIdx.y, gu_lds);
 }
 
@@ -724,7 +730,7 @@ bool pick_dn_grp(const ExpertLaunch& L, int items, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_gate_up(const ExpertLaunch& L, hipStream_t s) {
-    const int items = L.table != nullptr ? L.max_items
+    const int items = L.table != nullptr ? L.max_items + (L.gu_part != nullptr && L.maxt == 1 ? 1 : 0)
                                          : (L.n_tokens + kTileTok * L.maxt - 1) / (kTileTok * L.maxt);
     if (grp_ok(L) && pick_gu_grp(L, items, s)) return hipGetLastError();
     const dim3 grid(L.inter / kTileRows, items);

@@ -92,9 +92,16 @@ inline size_t gate_up_lds_bytes(int ksa, int maxt, int np_lds, int hidden) {
     return gate_up_red_bytes(ksa, maxt) + (maxt == 1 ? (size_t)np_lds * ((size_t)hidden * 2 + 16) : 0);
 }
 
-template <int NKB, int D, int MAXT, bool F16, bool XLDS, int KS, bool SINGLE, int KSA = KS, int TR = kTileRows>
+// PARTIAL (single mode): the tile covers k-part `kpart` of the row (KSA * NKB
+// k-blocks starting at kpart * KSA * NKB) and writes its fp32 gate and up
+// sums to L.gu_part[kpart][gate, up][token][row] instead of h; the parts are
+// summed in order and SiLU'd later (shared_h_finalize), so a small grid can
+// spread one expert's rows over twice the CUs.
+template <int NKB, int D, int MAXT, bool F16, bool XLDS, int KS, bool SINGLE, int KSA = KS,
+          int TR = kTileRows, bool PARTIAL = false>
 __device__ __forceinline__ void gate_up_tile(const ExpertLaunch& L, int tile, int item,
-                                             unsigned char* lds) {
+                                             unsigned char* lds, int kpart = 0) {
+    static_assert(!PARTIAL || (SINGLE && MAXT == 1), "k-part sums: single mode, <= 16 tokens");
     typedef Mma<F16> M;
     typedef typename M::V V;
     f32x4* red = reinterpret_cast<f32x4*>(lds);  // [KSA][MAXT][2][64]
@@ -107,7 +114,7 @@ __device__ __forceinline__ void gate_up_tile(const ExpertLaunch& L, int tile, in
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int g = lane >> 4, c = lane & 15;
     const bool active = KSA == KS || wave < KSA;  // wave-uniform
-    const int kb0 = (active ? wave : 0) * NKB;
+    const int kb0 = ((PARTIAL ? kpart * KSA : 0) + (active ? wave : 0)) * NKB;
 
     // TR = 8: lanes c and c + 8 read the same row (one fetch per wave
     // instruction); MFMA rows 8..15 are discarded
@@ -255,6 +262,17 @@ __device__ __forceinline__ void gate_up_tile(const ExpertLaunch& L, int tile, in
             U += red[((w * MAXT + tt) * 2 + 1) * 64 + lane];
         }
         const int q = tt * kTileTok + c;
+        if (PARTIAL) {
+            if (q < u.np && 4 * g < TR) {
+                const size_t p = (size_t)(u.pb + q), T = (size_t)L.n_tokens;
+                const int row = r0 + 4 * g;
+                *reinterpret_cast<float4*>(L.gu_part + (((size_t)kpart * 2 + 0) * T + p) * I + row) =
+                    float4{G[0], G[1], G[2], G[3]};
+                *reinterpret_cast<float4*>(L.gu_part + (((size_t)kpart * 2 + 1) * T + p) * I + row) =
+                    float4{U[0], U[1], U[2], U[3]};
+            }
+            continue;
+        }
         if (q < u.np && 4 * g < TR) {
             const size_t p = (size_t)(u.pb + q);
             const float wf = !SINGLE && L.fold_weight ? L.plan.pair_weight[p] : 1.0f;
@@ -280,5 +298,24 @@ __device__ __forceinline__ void gate_up_tile(const ExpertLaunch& L, int tile, in
     }
 }
 
+
+// h of the single-mode expert whose gate/up ran as k-part sums (PARTIAL):
+// rows [16*tile, 16*tile + 16) of every token, parts summed in order 0, 1, ...
+// One thread per (token, row); pairs are the tokens [0, n_tokens).
+__device__ __forceinline__ void shared_h_finalize(const ExpertLaunch& L, int tile) {
+    const int I = L.inter, T = L.n_tokens;
+    for (int cell = threadIdx.x; cell < kTileRows * T; cell += blockDim.x) {
+        const int t = cell / kTileRows, row = tile * kTileRows + cell % kTileRows;
+        float gate = 0.f, up = 0.f;
+        for (int kp = 0; kp < L.gu_kparts; ++kp) {
+            gate += L.gu_part[(((size_t)kp * 2 + 0) * T + t) * I + row];
+            up += L.gu_part[(((size_t)kp * 2 + 1) * T + t) * I + row];
+        }
+        const float h = (gate / (1.0f + expf(-gate))) * up;
+        const uint32_t hi = bf16_rne(h);
+        L.h_hi[(size_t)t * I + row] = static_cast<uint16_t>(hi);
+        L.h_lo[(size_t)t * I + row] = static_cast<uint16_t>(bf16_rne(h - __uint_as_float(hi << 16)));
+    }
+}
 
 }  // namespace cx

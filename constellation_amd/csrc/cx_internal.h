@@ -141,6 +141,10 @@ struct ExpertLaunch {
     int np_lds;                   // >0: stage up to np_lds activation rows per item in LDS
     int skip_shared;              // grouped mode: routed items only (shared expert done apart)
     int max_lds;                  // dynamic LDS per workgroup the device allows (0: unknown)
+    float* gu_part;               // k-part gate/up sums of the shared expert [kparts][2][T][inter]
+                                  // (written by the split stage-2 tiles; the routed gate/up
+                                  // launch finalises them into h when non-null)
+    int gu_kparts;
 };
 
 hipError_t launch_gate_up(const ExpertLaunch& L, hipStream_t s);
@@ -196,6 +200,10 @@ int route_max_experts();
 // are the tokens (pair t = token t, the plan's shared pairs).
 bool dec_route_ok(int n_experts, int n_group);
 bool dec_shared_ok(int hidden, int inter);
+// The shared expert's stage-2 gate/up can run as two k-parts (T <= 8):
+// ExpertLaunch::gu_part set on both the stage-2 record and the routed
+// gate/up launch, which then finalises the shared h.
+bool dec_shared_split_ok(int hidden, int inter, int n_tokens);
 // Activation rows the shared expert's gate/up tiles of stage 2 stage in LDS
 // (0: stream them from L2).
 int dec_sgu_np_lds(int hidden, int n_tokens, int max_lds);

@@ -36,6 +36,7 @@ constexpr int kRouteTB = 16;        // tokens per row workgroup
 constexpr int kMaxRouteExperts = 1024;
 constexpr int kDecMaxExperts = 256;  // decode planner: one thread per expert
 constexpr int kDecThreads = 1024;    // stage-2 workgroup: 16 selection waves
+constexpr int kDecSplitMaxTokens = 8;  // the k-part split stage 2 has 8 selection waves
 
 __device__ __forceinline__ bool better(double a, int ia, double b, int ib) {
     return a > b || (a == b && ia < ib);
@@ -1347,14 +1348,20 @@ __global__ __launch_bounds__(kRouteThreads) void k_dec_logits(FusedArgs A) {
 // table) is requested before its first barrier.  LDS (dynamic) is shared by
 // the two roles: the planner's DecPlanLds or the gate/up tile's reduction
 // tile and staged activations.
-template <int EPL, int NKB, int KSA, bool XLDS>
-__global__ __launch_bounds__(kDecThreads) void k_dec_select_sgu(FusedArgs A, ExpertLaunch SG) {
+// NTHR threads per workgroup (selection: one wave per token, so T <= NTHR/64);
+// KP > 1: each shared-expert tile is split into KP k-parts over KP blocks
+// (k-part sums finalised by the routed gate/up launch), so the expert's
+// 29 MB spread over 2x the CUs (one CU sustains ~22 GB/s of these loads).
+template <int EPL, int NKB, int KSA, bool XLDS, int NTHR = kDecThreads, int KP = 1>
+__global__ __launch_bounds__(NTHR) void k_dec_select_sgu(FusedArgs A, ExpertLaunch SG) {
     extern __shared__ __attribute__((aligned(16))) unsigned char dlds[];
     if (blockIdx.x > 0) {
         // activations streamed from L2 ride the ring too: keep it 2 deep so
-        // the 16-wave block stays within 128 registers
+        // the block stays within 128 registers
         constexpr int D = NKB < (XLDS ? 4 : 2) ? NKB : (XLDS ? 4 : 2);
-        gate_up_tile<NKB, D, 1, false, XLDS, kDecThreads / 64, true, KSA>(SG, blockIdx.x - 1, 0, dlds);
+        const int b = blockIdx.x - 1;
+        gate_up_tile<NKB, D, 1, false, XLDS, NTHR / 64, true, KSA, kTileRows, (KP > 1)>(
+            SG, b / KP, 0, dlds, b % KP);
         return;
     }
     DecPlanLds& S = *reinterpret_cast<DecPlanLds*>(dlds);
@@ -1364,13 +1371,13 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_select_sgu(FusedArgs A, Exp
     double* sC = sS + TE;                                               // [T][E]
     // 1) every global input at once: this thread's logits, bias and
     //    residency (<= 4 (token, expert) cells), the layer table
-    constexpr int kCells = kTileTok * kDecMaxExperts / kDecThreads;
+    constexpr int kCells = (NTHR / 64) * kDecMaxExperts / NTHR;  // T <= NTHR/64 tokens
     double lg[kCells];
     float bs[kCells];
     bool rs[kCells];
 #pragma unroll
     for (int r = 0; r < kCells; ++r) {
-        const int i = tid + r * kDecThreads, e = i % E;
+        const int i = tid + r * NTHR, e = i % E;
         if (i < TE) {
             lg[r] = A.logits[i];
             bs[r] = A.bias[e];
@@ -1382,7 +1389,7 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_select_sgu(FusedArgs A, Exp
     int nres_part = 0;
 #pragma unroll
     for (int r = 0; r < kCells; ++r) {
-        const int i = tid + r * kDecThreads;
+        const int i = tid + r * NTHR;
         if (i < TE) {
             expert_scores(lg[r], bs[r], rs[r], &sS[i], &sC[i]);
             nres_part += i < E && rs[r] ? 1 : 0;  // token 0's row counts each expert once
@@ -1395,7 +1402,7 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_select_sgu(FusedArgs A, Exp
     if (wave < T) {
         int nres = 0;
 #pragma unroll
-        for (int w = 0; w < kDecThreads / 64; ++w) nres += S.nres_w[w];
+        for (int w = 0; w < NTHR / 64; ++w) nres += S.nres_w[w];
         SelIn<EPL> in;
         sel_load_lds<EPL>(in, sS + (size_t)wave * E, sC + (size_t)wave * E, nres);
         const SelOut o = select_any_reg<EPL>(in, E, A.n_group, A.topk_group, K, A.norm, A.scale);
@@ -1503,6 +1510,15 @@ template <int EPL, int XLDS>
 void go_dec_select_h(const FusedArgs& A, const ExpertLaunch* sg, size_t lds, hipStream_t s) {
     ExpertLaunch none{};
     const ExpertLaunch& G = sg ? *sg : none;
+    if (sg != nullptr && G.gu_part != nullptr) {  // k-part split: 8-wave blocks, T <= 8
+        const dim3 grid(1 + 2 * (G.inter / kTileRows)), block(512);
+        switch (A.hidden / kKB) {
+            case 56: cx_launch((k_dec_select_sgu<EPL, 4, 7, XLDS, 512, 2>), grid, block, lds, s, A, G); break;
+            case 8: cx_launch((k_dec_select_sgu<EPL, 1, 4, XLDS, 512, 2>), grid, block, lds, s, A, G); break;
+            default: cx_launch((k_dec_select_sgu<EPL, 1, 2, XLDS, 512, 2>), grid, block, lds, s, A, G); break;
+        }
+        return;
+    }
     const dim3 grid(1 + (sg ? G.inter / kTileRows : 0)), block(kDecThreads);
     switch (A.hidden / kKB) {
         case 56: cx_launch((k_dec_select_sgu<EPL, 4, 14, XLDS>), grid, block, lds, s, A, G); break;
@@ -1511,11 +1527,12 @@ void go_dec_select_h(const FusedArgs& A, const ExpertLaunch* sg, size_t lds, hip
     }
 }
 
-int dec_select_ksa(int hidden) {
+// Active waves of a shared-expert tile in stage 2 (k-part split: per part).
+int dec_select_ksa(int hidden, bool split = false) {
     switch (hidden / kKB) {
-        case 56: return 14;
-        case 8: return 8;
-        default: return 4;
+        case 56: return split ? 7 : 14;
+        case 8: return split ? 4 : 8;
+        default: return split ? 2 : 4;
     }
 }
 
@@ -1524,7 +1541,8 @@ void go_dec_select(const FusedArgs& A, const ExpertLaunch* sg, hipStream_t s) {
     const bool xl = sg != nullptr && sg->np_lds > 0;
     size_t lds = sizeof(DecPlanLds) + (size_t)2 * A.n_tokens * A.n_experts * sizeof(double);
     if (sg != nullptr)
-        lds = std::max(lds, gate_up_lds_bytes(dec_select_ksa(A.hidden), 1, xl ? sg->np_lds : 0, A.hidden));
+        lds = std::max(lds, gate_up_lds_bytes(dec_select_ksa(A.hidden, sg->gu_part != nullptr), 1,
+                                              xl ? sg->np_lds : 0, A.hidden));
     if (xl) go_dec_select_h<EPL, true>(A, sg, lds, s);
     else go_dec_select_h<EPL, false>(A, sg, lds, s);
 }
@@ -1556,6 +1574,11 @@ int dec_sgu_np_lds(int hidden, int n_tokens, int max_lds) {
     return n_tokens <= rows ? n_tokens : 0;
 }
 
+bool dec_shared_split_ok(int hidden, int inter, int n_tokens) {
+    return dec_shared_ok(hidden, inter) && n_tokens <= kDecSplitMaxTokens &&
+           (hidden / kKB) % 2 == 0;
+}
+
 bool dec_shared_ok(int hidden, int inter) {
     const int nkh = hidden / kKB;
     if (hidden % kKB != 0 || (nkh != 56 && nkh != 8 && nkh != 4)) return false;
@@ -1573,6 +1596,8 @@ hipError_t launch_dec_logits(const RouteArgs& R, hipStream_t s) {
 
 hipError_t launch_dec_select_sgu(const RouteArgs& R, const ExpertLaunch* sg, hipStream_t s) {
     if (R.plan == nullptr || R.n_tokens > kTileTok || !dec_route_ok(R.n_experts, R.n_group))
+        return hipErrorInvalidValue;
+    if (sg != nullptr && sg->gu_part != nullptr && R.n_tokens > kDecSplitMaxTokens)
         return hipErrorInvalidValue;
     const FusedArgs A = fused_args(R);
     switch (register_epl(R.n_experts, R.n_group)) {

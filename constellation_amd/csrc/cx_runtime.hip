@@ -197,6 +197,7 @@ struct cx_ctx {
     int* err_flag = nullptr;           // device int: error bits of the device checks
     int max_lds = 65536;               // dynamic LDS budget per workgroup
     DevBuf plan_buf, hhi, hlo, ypart, logits, route_ids, route_w, hscratch;
+    DevBuf gu_part;                    // shared expert's k-part gate/up sums (decode)
     DevBuf dx, dy;                     // cx_expert_run_host staging (device)
     void* pin_x = nullptr;             // pinned host staging
     void* pin_y = nullptr;
@@ -381,6 +382,16 @@ int moe_decode(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, 
     SG.y_part = static_cast<float*>(ctx->ypart.p);
     SG.np_lds = route != nullptr ? dec_sgu_np_lds(layer->hidden, T, ctx->max_lds) : 0;
     const ExpertLaunch* sg = layer->has_shared ? &SG : nullptr;
+    // T <= 8 with the router: the shared gate/up tiles run as two k-parts
+    // (twice the CUs); the routed gate/up launch finalises the shared h
+    const bool split = route != nullptr && sg != nullptr &&
+                       dec_shared_split_ok(layer->hidden, layer->inter, T);
+    if (split) {
+        int rc = ensure(&ctx->gu_part, sizeof(float) * 2 * 2 * (size_t)T * layer->inter, s);
+        if (rc) return rc;
+        SG.gu_part = static_cast<float*>(ctx->gu_part.p);
+        SG.gu_kparts = 2;
+    }
     const int routed_items = std::min(T * top_k, layer->n_experts);
     if (route != nullptr) {
         route->plan = &P;
@@ -420,10 +431,13 @@ int moe_decode(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, 
     L.out_dtype = out_dtype;
     L.np_lds = np_lds;
     L.skip_shared = 1;
-    if (L.max_items > 0) {
+    L.gu_part = SG.gu_part;
+    L.gu_kparts = SG.gu_kparts;
+    if (L.max_items > 0 || L.gu_part != nullptr) {
         Span sp(ctx, "gate_up", s);
         CX_HIP(launch_gate_up(L, s));
     }
+    L.gu_part = nullptr;
     // down: the routed items and the shared expert's item (last)
     L.skip_shared = 0;
     L.max_items = routed_items + layer->has_shared;
@@ -773,7 +787,7 @@ int cx_ctx_destroy(cx_ctx* c) {
     (void)hipDeviceSynchronize();
     drain_spans(c);
     DevBuf* bufs[] = {&c->plan_buf, &c->hhi, &c->hlo, &c->ypart, &c->logits, &c->route_ids,
-                      &c->route_w, &c->hscratch, &c->dx, &c->dy};
+                      &c->route_w, &c->hscratch, &c->gu_part, &c->dx, &c->dy};
     for (DevBuf* b : bufs)
         if (b->p) (void)hipFree(b->p);
     if (c->err_flag) (void)hipFree(c->err_flag);
