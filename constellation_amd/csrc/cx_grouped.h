@@ -39,7 +39,7 @@ constexpr size_t grp_gu_lds() { return (size_t)2 * kGrpTiles * kActBlk; }  // 32
 // h enters as two planes (hi, lo), so a slot holds 2 x kGrpTiles blocks.
 constexpr int kDnGrpWaves = 8;
 constexpr int kDnGrpRows = kDnGrpWaves * 2 * kTileRows;  // 256
-constexpr int kDnGrpD = 3;
+constexpr int kDnGrpD = 4;
 constexpr size_t grp_dn_lds() { return (size_t)2 * 2 * kGrpTiles * kActBlk; }  // 64 KB
 
 // Barrier after this wave's LDS writes: the writes complete (lgkmcnt), no
@@ -280,7 +280,7 @@ __device__ __forceinline__ void grp_down_item(const ExpertLaunch& L, const Unit&
                                               unsigned char* lds) {
     typedef Mma<false> M;
     typedef M::V V;
-    constexpr int D = NKB >= 8 ? 4 : 2;
+    constexpr int D = NKB >= 8 ? kDnGrpD : 2;
     constexpr int PS = 4 + NT;
     constexpr size_t PLANE = (size_t)kGrpTiles * kActBlk;
     constexpr size_t SLOT = 2 * PLANE;
