@@ -196,6 +196,31 @@ def test_moe_layer_fused_router(gpu, oracle):
         _free(layer, experts, sh)
 
 
+def test_moe_layer_decode_back_to_back(gpu, oracle):
+    """The decode pipeline (T <= 16) reuses its plan, h, k-part and y_part
+    buffers on every call.  Twelve calls back to back with new tokens (and
+    T = 1, 2, 3 in turn), one sync at the end: each output must match the
+    oracle, which stale data from an earlier call would not."""
+    print("[moe] decode back to back", flush=True)
+    E, H, I = 32, 1024, 512
+    layer, experts, sh, cpu, cpu_sh = _make_layer(gpu, oracle, E, H, I, seed=41)
+    try:
+        _, w, bias = _router_inputs(gpu, 42, 1, E, H)
+        outs = []
+        for i in range(12):
+            x = gpu.gen_normal(43 + i, 3, (1 + i % 3, H), 1.0, torch.bfloat16)
+            _, yf, ids, wts = gpu.moe_layer(layer, x, w, bias, n_group=8, topk_group=4, top_k=8,
+                                            want_f32=True)
+            outs.append((x, yf, ids, wts))
+        gpu.sync()
+        for x, yf, ids, wts in outs:
+            ref = _oracle_moe(oracle, cpu, cpu_sh, x.float().cpu().numpy(), ids.cpu().numpy(),
+                              wts.cpu().numpy())
+            assert rel_l2(yf.cpu().numpy(), ref) < 1e-5
+    finally:
+        _free(layer, experts, sh)
+
+
 @pytest.mark.parametrize("prefill", [False, True])
 def test_moe_bad_and_missing_experts_reported(gpu, prefill):
     print(f"[moe] error flags prefill={prefill}", flush=True)
