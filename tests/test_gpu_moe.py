@@ -139,7 +139,8 @@ def _oracle_moe(oracle, cpu, cpu_sh, x_f32, ids, wts):
                                          (16, False, 512), (23, True, 512), (70, True, 512),
                                          (2, False, 256), (40, True, 256)])
 def test_moe_grouped_vs_oracle(gpu, oracle, T, prefill, I):
-    """T <= 16: fused decode down + combine (I=512) or per-pair + combine (I=256)."""
+    """T <= 16: the decode pipeline (I=512, a shape it compiles) or the general
+    per-item path (I=256); T > 16: the prefill grouped GEMM."""
     print(f"[moe] T={T} prefill={prefill} I={I}", flush=True)
     E, H = 32, 1024
     layer, experts, sh, cpu, cpu_sh = _make_layer(gpu, oracle, E, H, I, seed=11)
@@ -389,6 +390,54 @@ def test_full_size_moe_layer(gpu, oracle, T):
         assert np.array_equal(_bits(y), oracle.encode_act(yf, BF16, "rne"))
     finally:
         _free(layer, experts, sh)
+
+
+@pytest.mark.parametrize("T", [1, 16])
+def test_full_size_moe_layer_run_to_run_exact(gpu, oracle, T):
+    """The reference's router stability check (server/test/
+    1_smoke_moe_router_validation.py:16-17, 96-172): hidden = linspace(-1e-2,
+    1e-2, hidden_size) in the runtime dtype, the MoE layer run 10 times; the
+    top-k indices and weights must not change and the output must be finite.
+    Here the whole output is also bit-identical run to run (every reduction
+    has a fixed order), at DeepSeek-V3 shapes; T = 16 scales the row per token."""
+    print(f"[moe] run to run T={T}", flush=True)
+    E, H = 256, 7168
+    from constellation_amd.engine import Expert, Layer
+    experts = [Expert.generate(0, 83, 0x5000 + 4 * e) for e in range(E)]
+    sh = Expert.generate(0, 83, 0x5000 + 4 * E)
+    layer = Layer(gpu, experts, sh)
+    try:
+        _, w, bias = _router_inputs(gpu, 84, 1, E, H)
+        row = torch.linspace(-1e-2, 1e-2, H, dtype=torch.float32)
+        x = torch.stack([row * (1.0 + 0.25 * t) for t in range(T)]).to(torch.bfloat16).cuda()
+        runs = [gpu.moe_layer(layer, x, w, bias, n_group=8, topk_group=4, top_k=8,
+                              routed_scaling_factor=2.5, want_f32=True) for _ in range(10)]
+        gpu.sync()
+        y0, yf0, ids0, w0 = (t.cpu() for t in runs[0])
+        assert torch.isfinite(yf0).all()
+        for y, yf, ids, wts in runs[1:]:
+            assert torch.equal(ids.cpu(), ids0)
+            assert torch.equal(wts.cpu().view(torch.int32), w0.view(torch.int32))
+            assert torch.equal(y.cpu().view(torch.int16), y0.view(torch.int16))
+            assert torch.equal(yf.cpu().view(torch.int32), yf0.view(torch.int32))
+        for t, (oi, ow, margins, _) in enumerate(_oracle_route(oracle, x, w, bias)):
+            if min(margins) > 1e-12:
+                assert ids0[t].tolist() == oi.tolist(), t
+    finally:
+        _free(layer, experts, sh)
+
+
+def test_device_probe_invariants(gpu):
+    """The reference's device-probe invariants (cpu/tests/test_gpu_info_cpu_v2.cc:
+    40-100): a non-empty name, total and free memory above zero; plus the
+    gfx950 architecture and its fp16/bf16/fp8 capability bits."""
+    from constellation_amd.engine import device_count, device_info
+    assert device_count() >= 1
+    info = device_info(0)
+    assert info["name"] and info["arch"].startswith("gfx950")
+    assert info["total_mem_bytes"] > 0 and 0 < info["free_mem_bytes"] <= info["total_mem_bytes"]
+    assert info["compute_units"] > 0
+    assert info["capability_flags"] & 0x7 == 0x7
 
 
 def test_full_size_prefill_grouped_items(gpu, oracle):

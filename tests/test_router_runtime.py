@@ -109,3 +109,17 @@ def test_route_tokens_batched_equals_single(gpu):
         routes = route_token_real(xs[t], w, b, **KW)
         assert [e for e, _ in routes] == ids[t].tolist()
         assert [x for _, x in routes] == wts[t].tolist()
+
+
+@pytest.mark.gpu
+def test_route_token_real_run_to_run_exact():
+    """The reference's stability check (server/test/1_smoke_moe_router_validation.py:
+    16-17, 96-162): hidden = linspace(-1e-2, 1e-2, hidden_size), routed 10 times;
+    the routes (ids and weights) must be identical run to run."""
+    print("[route_token_real] run to run", flush=True)
+    _, w, b = _cpu_inputs()
+    hidden = torch.linspace(-1e-2, 1e-2, 7168, dtype=torch.float32).cuda()
+    w, b = w.cuda(), b.cuda()
+    runs = [route_token_real(hidden, w, b, **KW) for _ in range(10)]
+    assert len(runs[0]) == 8
+    assert all(r == runs[0] for r in runs[1:])
