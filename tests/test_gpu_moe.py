@@ -360,10 +360,12 @@ def test_moe_decode_given_routes_with_shared(gpu, oracle, T, dtype):
         _free(layer, experts, sh)
 
 
-@pytest.mark.parametrize("T", [1, 16])
+@pytest.mark.parametrize("T", [1, 3, 8, 9, 16])
 def test_full_size_moe_layer(gpu, oracle, T):
     """The benchmark path at DeepSeek-V3 shapes: cx_moe_layer with 256 resident
-    experts + shared, H=7168, I=2048, bf16 router (config 1 / config 2)."""
+    experts + shared, H=7168, I=2048, bf16 router (config 1 / config 2).  T
+    spans the decode regimes: activation rows staged in LDS (T <= 3), the
+    shared expert's two-k-part stage 2 (T <= 8) and its full-K form (T > 8)."""
     print(f"[moe] full-size layer T={T}", flush=True)
     E, H = 256, 7168
     from constellation_amd.engine import Expert, Layer
