@@ -429,6 +429,89 @@ def test_full_size_moe_layer_run_to_run_exact(gpu, oracle, T):
         _free(layer, experts, sh)
 
 
+def _sample_tokens(ids, T, n_hot=4, n_spread=4):
+    """The hottest expert's first n_hot tokens plus n_spread evenly spread ones."""
+    flat = ids[ids >= 0]
+    hot = int(np.bincount(flat).argmax())
+    hot_tok = [t for t in range(T) if hot in ids[t]][:n_hot]
+    spread = [int(v) for v in np.linspace(0, T - 1, n_spread)]
+    return sorted(set(hot_tok + spread))
+
+
+def test_config3_prefill_chunk_matches_oracle(gpu, oracle):
+    """The config-3 benchmark call: 512 tokens through cx_moe_layer with a
+    Zipf-skewed correction bias, 256 experts + shared at DeepSeek-V3 shapes
+    (hot experts split into several 64-pair items).  Every token's routes
+    against the oracle; the output of a token sample that includes the hottest
+    expert's tokens against the dequantise-then-fp32 oracle."""
+    print("[moe] config-3 prefill chunk", flush=True)
+    E, H, T = 256, 7168, 512
+    from constellation_amd.engine import Expert, Layer
+    experts = [Expert.generate(0, 85, 0x6000 + 4 * e) for e in range(E)]
+    sh = Expert.generate(0, 85, 0x6000 + 4 * E)
+    layer = Layer(gpu, experts, sh)
+    try:
+        x, w, bias = _router_inputs(gpu, 86, T, E, H, bias_skew=0.25)
+        y, yf, ids, wts = gpu.moe_layer(layer, x, w, bias, n_group=8, topk_group=4, top_k=8,
+                                        routed_scaling_factor=2.5, want_f32=True)
+        gpu.sync()
+        idn, wn = ids.cpu().numpy(), wts.cpu().numpy()
+        assert np.bincount(idn[idn >= 0]).max() > 64  # a hot expert spans several items
+        for t, (oi, ow, margins, _) in enumerate(_oracle_route(oracle, x, w, bias)):
+            if min(margins) > 1e-12:
+                assert idn[t].tolist() == oi.tolist(), t
+                assert np.allclose(wn[t], ow, rtol=1e-6, atol=0), t
+        sample = _sample_tokens(idn, T)
+        used = sorted(set(idn[sample].ravel().tolist()) - {-1})
+        cpu = {e: oracle.gen_expert(85, 0x6000 + 4 * e) for e in used}
+        cpu_sh = oracle.gen_expert(85, 0x6000 + 4 * E)
+        ref = _oracle_moe(oracle, [cpu.get(e) for e in range(E)], cpu_sh,
+                          x.float().cpu().numpy()[sample], idn[sample], wn[sample])
+        got = yf.cpu().numpy()[sample]
+        assert rel_l2(got, ref) < 1e-5 and np.abs(got - ref).max() < 2e-2
+        assert np.array_equal(_bits(y)[sample], oracle.encode_act(got, BF16, "rne"))
+    finally:
+        _free(layer, experts, sh)
+
+
+def test_config4_node_share_layer_matches_oracle(gpu, oracle):
+    """One layer of the config-4 node share: 64 resident experts of 256 (e = 0
+    mod 4), no shared expert, 32 tokens routed under the resident mask with a
+    Zipf-skewed bias (the grouped path).  Routes against the oracle's masked
+    router; a token sample against the oracle."""
+    print("[moe] config-4 node-share layer", flush=True)
+    E, H, T = 256, 7168, 32
+    from constellation_amd.engine import Expert, Layer
+    res = np.zeros(E, np.uint8)
+    res[::4] = 1
+    experts = [Expert.generate(0, 87, 0x7000 + 4 * e) if res[e] else None for e in range(E)]
+    layer = Layer(gpu, experts, None)
+    try:
+        x, w, bias = _router_inputs(gpu, 88, T, E, H, bias_skew=0.25)
+        y, yf, ids, wts = gpu.moe_layer(layer, x, w, bias, resident=torch.from_numpy(res).cuda(),
+                                        n_group=8, topk_group=4, top_k=8, routed_scaling_factor=2.5,
+                                        want_f32=True)
+        gpu.sync()
+        idn, wn = ids.cpu().numpy(), wts.cpu().numpy()
+        assert all(res[e] for e in idn[idn >= 0])
+        for t, (oi, ow, margins, _) in enumerate(_oracle_route(oracle, x, w, bias, resident=res)):
+            if min(margins) > 1e-12:
+                assert idn[t][:len(oi)].tolist() == oi.tolist(), t
+        sample = _sample_tokens(idn, T)
+        used = sorted(set(idn[sample].ravel().tolist()) - {-1})
+        cpu = {e: oracle.gen_expert(87, 0x7000 + 4 * e) for e in used}
+        ref = _oracle_moe(oracle, [cpu.get(e) for e in range(E)], None,
+                          x.float().cpu().numpy()[sample], idn[sample], wn[sample])
+        got = yf.cpu().numpy()[sample]
+        assert rel_l2(got, ref) < 1e-5 and np.abs(got - ref).max() < 2e-2
+    finally:
+        torch.cuda.synchronize()
+        layer.close()
+        for e in experts:
+            if e is not None:
+                e.free()
+
+
 def test_device_probe_invariants(gpu):
     """The reference's device-probe invariants (cpu/tests/test_gpu_info_cpu_v2.cc:
     40-100): a non-empty name, total and free memory above zero; plus the
