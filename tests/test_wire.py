@@ -105,3 +105,48 @@ def test_malformed_bodies_rejected_by_both_sides(case):
     if case in ("truncated", "trailing", "n_routes", "act_nbytes", "empty"):
         with pytest.raises(P.ProtocolError):
             P.decode_moe_layer_request(bad)
+
+
+def test_random_and_mutated_bodies_never_crash_and_agree():
+    """Fuzz of the node-side decoder, which reads bytes off the network: random
+    bodies and single-field mutations of valid ones either decode to exactly
+    what the Python codec reads, or are rejected by both sides; nothing reads
+    out of bounds (the decoder gets the exact buffer length)."""
+    from constellation_amd import CxError
+    rng = np.random.default_rng(1234)
+    bodies = []
+    for i in range(300):  # random lengths and bytes, header-sized and up
+        bodies.append(rng.integers(0, 256, int(rng.integers(0, 96)), dtype=np.uint8).tobytes())
+    for i in range(300):  # valid bodies with one header word replaced, or cut / padded
+        T, H, K = int(rng.integers(1, 5)), int(rng.choice([32, 64])), int(rng.integers(0, 9))
+        body = bytearray(P.encode_moe_layer_request(_msg(T, H, K, seed=i)))
+        kind = i % 3
+        if kind == 0:
+            w = int(rng.integers(0, 9))
+            v = int(rng.choice([0, 1, 2, 3, 64, 65, 0x7FFFFFFF, 0xFFFFFFFF, int(rng.integers(0, 1 << 32))]))
+            at = 4 * w if w < 8 else 32 + 8 * T * K
+            body[at:at + 4] = v.to_bytes(4, "little")
+        elif kind == 1:
+            body = body[:int(rng.integers(0, len(body)))]
+        else:
+            body = body + bytes(int(rng.integers(1, 9)))
+        bodies.append(bytes(body))
+    accepted = 0
+    for body in bodies:
+        try:
+            py = P.decode_moe_layer_request(body)
+        except P.ProtocolError:
+            py = None
+        try:
+            info = _peek(body)
+        except CxError:
+            info = None
+        if info is None:
+            continue
+        accepted += 1
+        assert py is not None
+        assert (info.layer_id, info.batch_size, info.hidden_dim, info.top_k) == \
+            (py["layer_id"], py["batch_size"], py["hidden_dim"], py["top_k"])
+        assert len(body) == 32 + 8 * py["batch_size"] * py["top_k"] + 4 + \
+            py["batch_size"] * py["hidden_dim"] * 2
+    assert accepted > 0
