@@ -194,9 +194,10 @@ def bench_single_expert(ctx, layers, steps):
     for i in range(steps):
         ctx.expert_run(experts[i % 64], x)
     torch.cuda.synchronize()
-    gu, dn = ctx.profile_read("gate_up"), ctx.profile_read("down")
+    # one launch ("expert") at 1..3 tokens, else gate/up + down
+    fx, gu, dn = ctx.profile_read("expert"), ctx.profile_read("gate_up"), ctx.profile_read("down")
     ctx.profile(False)
-    dev_us = (gu[1] + dn[1]) * 1e3 / gu[0]
+    dev_us = (fx[1] + gu[1] + dn[1]) * 1e3 / steps
     alg = EXPERT_BYTES + 2 * H * 2
     xh = x.cpu().to(torch.float16).view(torch.int16).numpy().tobytes()
     for i in range(8):
@@ -206,8 +207,8 @@ def bench_single_expert(ctx, layers, steps):
     for i in range(n):
         ctx.expert_run_host(experts[i % 64], xh, FP16, 1, FP16)
     host_us = (time.perf_counter() - t0) / n * 1e6
-    return {"device_us_per_expert": dev_us, "gate_up_us": gu[1] * 1e3 / gu[0],
-            "down_us": dn[1] * 1e3 / dn[0], "algorithmic_bytes": alg,
+    return {"device_us_per_expert": dev_us, "launches_per_expert": (fx[0] + gu[0] + dn[0]) / steps,
+            "algorithmic_bytes": alg,
             "gbs": alg / (dev_us * 1e-6) / 1e9,
             "host_buffer_us_per_request": host_us,
             "host_buffer_note": "cx_expert_run_host, fp16 in/out, wall clock incl. pinned "

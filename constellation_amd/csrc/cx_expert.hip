@@ -458,6 +458,138 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 }
 
 // ---------------------------------------------------------------------------
+// One expert at 1..4 tokens (single mode), as two launches in which every
+// wave's weights are one round trip of loads.  At this size the launches are
+// bound by per-wave latency and MFMA work, not by HBM: the 16-row x full-K
+// waves of k_gate_up_t<14, 4> / k_down_item take ~10 and ~7 us even with all
+// 44 MB resident in the MALL.
+//  * Gate/up (k_gate_up_kpart): 2 k-parts x inter/16 tiles of 8-wave
+//    workgroups (KSA active waves x NKB k-blocks, the shared-expert split of
+//    k_dec_select_sgu), fp32 part sums to L.gu_part[kpart][gate, up][t][row].
+//    Twice the workgroups of one 16-row tile per workgroup, so every CU
+//    streams; K over 8 waves of one workgroup instead keeps half the CUs idle.
+//  * Down (k_down_ks): workgroup = 2 row groups of 16 output rows x 4 k
+//    ranges (8 waves, NKBW k-blocks each, all loads in flight at once).  The
+//    waves of a k range first turn its part sums into h = silu(g0 + g1) *
+//    (u0 + u1) (the order of shared_h_finalize), bf16 hi + lo, in a shared
+//    LDS slice, half each; the 4 partial tiles of a row group are summed in
+//    LDS in k order.
+template <int NKB, int KSA, bool F16, bool XLDS>
+__global__ __launch_bounds__(512) void k_gate_up_kpart(ExpertLaunch L) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char gk_lds[];
+    gate_up_tile<NKB, (NKB < 4 ? NKB : 4), 1, F16, XLDS, 8, true, KSA, kTileRows, true>(
+        L, blockIdx.x, 0, gk_lds, blockIdx.y);
+}
+
+constexpr int kDownKsRows = 4;   // tokens of the split-K down launch
+constexpr int kDownKsGroups = 2;  // 16-row groups per workgroup
+
+inline size_t down_ks_lds(int nkbw) {
+    return (size_t)4 * 2 * kDownKsRows * ((size_t)nkbw * kKB * 2 + 16) + (size_t)4 * kDownKsGroups * 64 * 16;
+}
+
+template <int NKBW>
+__global__ __launch_bounds__(512) void k_down_ks(ExpertLaunch L) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char dk_lds[];
+    constexpr int KW = NKBW * kKB;      // k per range
+    constexpr size_t HS = KW * 2 + 16;  // LDS row stride (bytes) of one h plane
+    constexpr int NI = KW / 4;          // 4-k items per token and range
+    constexpr int ITEMS = (NI + 127) / 128;
+    const int H = L.hidden, I = L.inter, np = L.n_tokens;
+    const cx_expert_desc& e = L.single;
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int rg = wave >> 2, kq = wave & 3;
+    const int g = lane >> 4, c = lane & 15;
+    const int r0 = (blockIdx.x * kDownKsGroups + rg) * kTileRows;
+    const int kb0 = kq * NKBW;
+    unsigned char* hw = dk_lds + (size_t)kq * (2 * kDownKsRows * HS);
+    f32x4* red = reinterpret_cast<f32x4*>(dk_lds + 4 * (2 * kDownKsRows * HS));  // [8][64]
+    // 1) part sums of this wave's half of the k range (older than the weight
+    //    loads, so waiting for them leaves the weights in flight)
+    const size_t T = (size_t)np;
+    const float* gp = L.gu_part + (size_t)kb0 * kKB;
+    float4 pg0[kDownKsRows][ITEMS], pg1[kDownKsRows][ITEMS], pu0[kDownKsRows][ITEMS], pu1[kDownKsRows][ITEMS];
+#pragma unroll
+    for (int q = 0; q < kDownKsRows; ++q) {
+        if (q < np) {
+#pragma unroll
+            for (int it = 0; it < ITEMS; ++it) {
+                const int i = it * 128 + rg * 64 + lane;
+                if (NI % 128 != 0 && i >= NI) continue;
+                const size_t k4 = (size_t)i * 4;
+                pg0[q][it] = *reinterpret_cast<const float4*>(gp + ((0 * 2 + 0) * T + q) * I + k4);
+                pg1[q][it] = *reinterpret_cast<const float4*>(gp + ((1 * 2 + 0) * T + q) * I + k4);
+                pu0[q][it] = *reinterpret_cast<const float4*>(gp + ((0 * 2 + 1) * T + q) * I + k4);
+                pu1[q][it] = *reinterpret_cast<const float4*>(gp + ((1 * 2 + 1) * T + q) * I + k4);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 2) this wave's 16 rows x KW of Wd, all in flight
+    const uint8_t* pd = e.w_down + (size_t)(r0 + c) * I + (size_t)kb0 * kKB + g * 32;
+    u32x4 wb[NKBW][2];
+#pragma unroll
+    for (int k = 0; k < NKBW; ++k) {
+        wb[k][0] = ld16(pd + k * kKB);
+        wb[k][1] = ld16(pd + k * kKB + 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int rbd = __builtin_amdgcn_readfirstlane(r0 / e.down_rb);
+    const float* sd = e.s_down + (size_t)rbd * (I / kKB) + kb0;
+    float scd[NKBW];
+#pragma unroll
+    for (int k = 0; k < NKBW; ++k) scd[k] = ldsc(sd + k);
+    // 3) h = silu(gate) * up, bf16 hi + lo, into the k range's LDS slice
+#pragma unroll
+    for (int q = 0; q < kDownKsRows; ++q) {
+        if (q < np) {
+#pragma unroll
+            for (int it = 0; it < ITEMS; ++it) {
+                const int i = it * 128 + rg * 64 + lane;
+                if (NI % 128 != 0 && i >= NI) continue;
+                const float4 a = pg0[q][it], b = pg1[q][it], u = pu0[q][it], v = pu1[q][it];
+                const float gs[4] = {a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w};
+                const float us[4] = {u.x + v.x, u.y + v.y, u.z + v.z, u.w + v.w};
+                uint32_t hi[4], lo[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float h = (gs[j] / (1.0f + expf(-gs[j]))) * us[j];
+                    hi[j] = bf16_rne(h);
+                    lo[j] = bf16_rne(h - __uint_as_float(hi[j] << 16));
+                }
+                const size_t off = (size_t)i * 8;
+                *reinterpret_cast<uint2*>(hw + q * HS + off) = uint2{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
+                *reinterpret_cast<uint2*>(hw + (kDownKsRows + q) * HS + off) =
+                    uint2{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
+            }
+        }
+    }
+    __syncthreads();
+    // 4) MFMA steps over this wave's rows and k range
+    const size_t hrow = (size_t)min(c, np - 1);
+    const unsigned char* lh = hw + hrow * HS + g * 64;
+    const unsigned char* ll = hw + (kDownKsRows + hrow) * HS + g * 64;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < NKBW; ++k) {
+        u32x4 hb[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            hb[j] = *reinterpret_cast<const u32x4*>(lh + k * (kKB * 2) + 16 * j);
+            hb[4 + j] = *reinterpret_cast<const u32x4*>(ll + k * (kKB * 2) + 16 * j);
+        }
+        acc += scd[k] * down_step(wb[k], hb);
+    }
+    red[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (kq == 0 && c < np) {
+        const f32x4* rr = red + rg * 4 * 64;
+        const f32x4 sum = ((rr[lane] + rr[64 + lane]) + rr[128 + lane]) + rr[192 + lane];
+        store_out4(L.y, L.y_f32, (size_t)c * H + r0 + 4 * g, sum, L.out_dtype);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Grouped GEMM for items of up to 64 pairs (cx_grouped.h): gate/up over
 // inter/64 row tiles x items as a one-dimensional XCD-aware grid
 // (xcd_tile_item: an item's x rows stay in one L2), down over grid =
@@ -760,6 +892,60 @@ hipError_t launch_down(const ExpertLaunch& L, hipStream_t s) {
         if (L.maxt == 1) cx_launch((k_down_rt<1>), grid, dim3(256), 0, s, L);
         else cx_launch((k_down_rt<4>), grid, dim3(256), 0, s, L);
     }
+    return hipGetLastError();
+}
+
+// Single mode at 1..4 tokens with 128-column k-blocks that split evenly into
+// 2 k-parts (gate/up) and 4 k ranges (down).  The launchers also need
+// L.gu_part (2 k-parts).
+bool expert_small_ok(const ExpertLaunch& L) {
+    if (L.table != nullptr || L.maxt != 1 || L.n_tokens < 1 || L.n_tokens > kDownKsRows) return false;
+    if (L.hidden % (kDownKsGroups * kTileRows) != 0) return false;
+    const int nkg = L.hidden / kKB, nkd = L.inter / kKB;
+    return (nkg == 56 || nkg == 8 || nkg == 4) && (nkd == 16 || nkd == 4);
+}
+
+namespace {
+
+template <int NKB, int KSA, bool F16>
+void go_gate_up_kpart(const ExpertLaunch& L, hipStream_t s) {
+    const dim3 grid(L.inter / kTileRows, 2), block(512);
+    if (L.np_lds >= L.n_tokens) {
+        cx_launch((k_gate_up_kpart<NKB, KSA, F16, true>), grid, block,
+                  gate_up_lds_bytes(KSA, 1, L.np_lds, L.hidden), s, L);
+    } else {
+        cx_launch((k_gate_up_kpart<NKB, KSA, F16, false>), grid, block,
+                  gate_up_lds_bytes(KSA, 1, 0, L.hidden), s, L);
+    }
+}
+
+template <bool F16>
+void pick_gate_up_kpart(const ExpertLaunch& L, hipStream_t s) {
+    switch (L.hidden / kKB) {
+        case 56: go_gate_up_kpart<4, 7, F16>(L, s); break;  // 2 x 7 waves x 4 k-blocks
+        case 8: go_gate_up_kpart<1, 4, F16>(L, s); break;
+        default: go_gate_up_kpart<1, 2, F16>(L, s); break;  // 4 k-blocks
+    }
+}
+
+bool small_args_ok(const ExpertLaunch& L) {
+    return expert_small_ok(L) && L.gu_part != nullptr && L.gu_kparts == 2;
+}
+
+}  // namespace
+
+hipError_t launch_gate_up_kpart(const ExpertLaunch& L, hipStream_t s) {
+    if (!small_args_ok(L)) return hipErrorInvalidValue;
+    if (L.in_dtype == CX_DTYPE_FP16) pick_gate_up_kpart<true>(L, s);
+    else pick_gate_up_kpart<false>(L, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_down_ks(const ExpertLaunch& L, hipStream_t s) {
+    if (!small_args_ok(L)) return hipErrorInvalidValue;
+    const dim3 grid(L.hidden / (kDownKsGroups * kTileRows)), block(512);
+    if (L.inter / kKB == 16) cx_launch((k_down_ks<4>), grid, block, down_ks_lds(4), s, L);
+    else cx_launch((k_down_ks<1>), grid, block, down_ks_lds(1), s, L);
     return hipGetLastError();
 }
 

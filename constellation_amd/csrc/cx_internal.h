@@ -164,6 +164,13 @@ hipError_t launch_plan(const int32_t* ids, const float* w, int n_tokens, int top
                        int item_cap, int max_items, PlanPtrs plan, int* err_flag,
                        hipStream_t s);
 
+// One expert at 1..4 tokens (single mode): gate/up as 2 k-part sums
+// (L.gu_part, L.gu_kparts = 2), then down with K split over the waves of each
+// workgroup, h finalised from the part sums.
+bool expert_small_ok(const ExpertLaunch& L);
+hipError_t launch_gate_up_kpart(const ExpertLaunch& L, hipStream_t s);
+hipError_t launch_down_ks(const ExpertLaunch& L, hipStream_t s);
+
 // Generic (any shape, any block size) single-expert path: correctness only.
 hipError_t launch_generic_expert(const cx_expert_desc& e, const void* x, int in_dtype,
                                  int n_tokens, float* h_scratch, void* y, int out_dtype,

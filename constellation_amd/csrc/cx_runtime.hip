@@ -872,6 +872,18 @@ int cx_expert_run(cx_ctx* ctx, const cx_expert_desc* expert, const void* x, int 
     L.out_dtype = out_dtype;
     L.np_lds = L.maxt == 1 ? lds_rows(ctx, expert->hidden, n_tokens) : 0;
     L.max_lds = ctx->max_lds;
+    if (expert_small_ok(L)) {
+        if ((rc = ensure(&ctx->gu_part, sizeof(float) * 2 * 2 * (size_t)n_tokens * I, s))) return rc;
+        L.gu_part = static_cast<float*>(ctx->gu_part.p);
+        L.gu_kparts = 2;
+        {
+            Span sp(ctx, "gate_up", s);
+            CX_HIP(launch_gate_up_kpart(L, s));
+        }
+        Span sp(ctx, "down", s);
+        CX_HIP(launch_down_ks(L, s));
+        return CX_OK;
+    }
     {
         Span sp(ctx, "gate_up", s);
         CX_HIP(launch_gate_up(L, s));

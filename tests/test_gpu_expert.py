@@ -97,14 +97,20 @@ def test_seeded_config0_expert(gpu, oracle):
         yf = yf.cpu().numpy()
         assert rel_l2(yf, yref) <= 1e-2 and np.abs(yf - yref).max() <= 2e-2
         assert rel_l2(yf, yref) < 1e-5, rel_l2(yf, yref)
-        # bf16 output = RNE of our fp32 output, and within 1 ulp of the reference's
+        # bf16 output = RNE of our fp32 output
         assert np.array_equal(_bits(y)[0], oracle.encode_act(yf[0], BF16, "rne"))
         # ulp distance in bf16 (sign-magnitude bits mapped to a monotone integer line)
         def line(b):
             b = b.astype(np.int32)
             return np.where(b & 0x8000, -(b & 0x7FFF), b)
-        ulp = np.abs(line(_bits(y)[0]) - line(g["y_bf16"]))
-        assert ulp.max() <= 1, ulp.max()
+        # Both fp32 pipelines (ours and the golden's) sit within 1 bf16 ulp of the
+        # correctly rounded float64 result; where they fall on opposite sides of a
+        # rounding midpoint they are 2 ulps apart, so each is held to the exact value.
+        _, y64 = expert_f64(cpu, xf, oracle.fp8_lut)
+        exact = line(oracle.encode_act(np.asarray(y64, np.float64).ravel().astype(np.float32), BF16, "rne"))
+        assert np.abs(line(_bits(y)[0]) - exact).max() <= 1
+        assert np.abs(line(g["y_bf16"]) - exact).max() <= 1
+        assert (_bits(y)[0] != g["y_bf16"]).sum() <= 64
     finally:
         e.free()
 
@@ -172,5 +178,108 @@ def test_run_host_contract(gpu, oracle):
         assert rel_l2(oracle.decode_act(got, FP16), yref) < 1e-3
         with pytest.raises(CxError):
             gpu.expert_run_host(e, xb.tobytes()[:-2], FP16, 3, FP16)
+    finally:
+        e.free()
+
+
+def _full_expert(seed, stream):
+    from constellation_amd.engine import Expert
+    return Expert.generate(0, seed, stream)
+
+
+def _x4(gpu, stream, dt):
+    x = gpu.gen_normal(12, stream, (4, 7168), 1.0, torch.bfloat16)
+    return x if dt == BF16 else x.to(torch.float16)
+
+
+@pytest.mark.parametrize("in_dt", [BF16, FP16])
+def test_small_batch_expert_full_size(gpu, oracle, in_dt):
+    """1..4 tokens take the k-part gate/up + split-K down launches (activations
+    staged in LDS up to 3 tokens, through the weight ring at 4); 5 tokens the
+    16-row full-K ones.  Every row against the oracle, and each token's row
+    must not depend on the batch it came in (T = 1 vs the first row of T = 4,
+    to the fp32 bit: the tokens are independent MFMA columns)."""
+    print(f"[small] full size T=1..5 in={in_dt}", flush=True)
+    e = _full_expert(11, 0x700)
+    try:
+        x5 = gpu.gen_normal(12, 0x710, (5, 7168), 1.0, torch.bfloat16)
+        if in_dt == FP16:
+            x5 = x5.to(torch.float16)
+        outs = {T: gpu.expert_run(e, x5[:T], want_f32=True) for T in (1, 2, 3, 4, 5)}
+        gpu.sync()
+        cpu = oracle.gen_expert(11, 0x700)
+        _, yref = oracle.expert_ref(cpu, oracle.decode_act(_bits(x5), in_dt))
+        for T, (y, yf) in outs.items():
+            yf = yf.cpu().numpy()
+            assert rel_l2(yf, yref[:T]) < 1e-5, (T, rel_l2(yf, yref[:T]))
+            assert np.abs(yf - yref[:T]).max() <= 2e-2
+            assert np.array_equal(_bits(y), oracle.encode_act(yf, in_dt, "rne")), T
+        for T in (2, 3, 4):
+            assert torch.equal(outs[T][1][0], outs[1][1][0]), T
+    finally:
+        e.free()
+
+
+def test_small_batch_expert_back_to_back(gpu, oracle):
+    """Calls queued without a sync between them, alternating tokens (1..4),
+    two full-size experts and a small one (other tile counts; the k-part sums
+    buffer is shared by all of them): every output must equal the same call
+    made alone."""
+    print("[small] back to back", flush=True)
+    big = [_full_expert(21, 0x720), _full_expert(22, 0x740)]
+    ex_s = oracle.gen_expert(77, 0x500, hidden=1024, inter=512)
+    small = _upload(ex_s)
+    try:
+        xs_big = _x4(gpu, 0x760, BF16)
+        xs_small = gpu.gen_normal(13, 0x770, (4, 1024), 1.0, torch.bfloat16)
+        cases = [(big[0], xs_big), (small, xs_small), (big[1], xs_big)]
+        ref = {}
+        for c, (e, x) in enumerate(cases):
+            for T in (1, 2, 3, 4):
+                ref[c, T] = gpu.expert_run(e, x[:T], want_f32=True)[1]
+                torch.cuda.synchronize()
+        got = []
+        for i in range(48):
+            c, T = i % 3, 1 + (i // 3) % 4
+            e, x = cases[c]
+            got.append((c, T, gpu.expert_run(e, x[:T], want_f32=True)[1]))
+        gpu.sync()
+        for c, T, yf in got:
+            assert torch.equal(yf, ref[c, T]), (c, T)
+        _, yref = oracle.expert_ref(ex_s, oracle.decode_act(_bits(xs_small), BF16))
+        assert rel_l2(ref[1, 4].cpu().numpy(), yref) < 1e-5
+    finally:
+        for e in (*big, small):
+            e.free()
+
+
+def test_small_batch_expert_graph_replay(gpu):
+    """The one-token expert captured in a HIP graph (two kernel nodes, no
+    memset nodes): replays with new activations, eager calls and syncs in
+    between; every replay must equal the eager result bit for bit."""
+    print("[small] graph replay", flush=True)
+    import ctypes as C
+    from constellation_amd._lib import lib, check
+    e = _full_expert(31, 0x780)
+    try:
+        xs = _x4(gpu, 0x790, BF16)
+        x = xs[:1].clone()
+        y = torch.empty((1, 7168), dtype=torch.bfloat16, device="cuda")
+        yf = torch.empty((1, 7168), dtype=torch.float32, device="cuda")
+        gpu.expert_run(e, x)  # context buffers exist before the capture
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            check(lib().cx_expert_run(gpu.handle, C.byref(e.desc), x.data_ptr(), BF16, 1,
+                                      y.data_ptr(), BF16, yf.data_ptr(), gpu.stream()))
+        for i in range(4):
+            x.copy_(xs[i:i + 1])
+            graph.replay()
+            torch.cuda.synchronize()
+            yr, yfr = gpu.expert_run(e, xs[i:i + 1], want_f32=True)
+            torch.cuda.synchronize()
+            assert torch.equal(yf, yfr), i
+            assert torch.equal(y.view(torch.int16), yr.view(torch.int16)), i
+        gpu.sync()
     finally:
         e.free()
