@@ -283,3 +283,27 @@ def test_small_batch_expert_graph_replay(gpu):
         gpu.sync()
     finally:
         e.free()
+
+
+@pytest.mark.parametrize("in_dt,out_dt", [(BF16, BF16), (FP16, FP16)])
+@pytest.mark.parametrize("H", [512, 1024])
+def test_small_batch_expert_small_dims(gpu, oracle, H, in_dt, out_dt):
+    """The 1..4-token launches at the other instantiated shapes (hidden 512:
+    2 waves x 1 k-block per k-part; inter 512: one k-block per down k range,
+    a quarter of the lanes finalising h)."""
+    print(f"[small] H={H} in={in_dt} out={out_dt}", flush=True)
+    ex = oracle.gen_expert(79, 0x520, hidden=H, inter=512)
+    e = _upload(ex)
+    try:
+        xb = oracle.gen_normal(80, 4, 4 * H, 1.0, "bf16" if in_dt == BF16 else "fp16").reshape(4, H)
+        x = _to_dev_bits(xb, in_dt)
+        _, yref = oracle.expert_ref(ex, oracle.decode_act(xb, in_dt))
+        for T in (1, 2, 3, 4):
+            y, yf = gpu.expert_run(e, x[:T], out_dtype=TDT[out_dt], want_f32=True)
+            torch.cuda.synchronize()
+            yf = yf.cpu().numpy()
+            assert rel_l2(yf, yref[:T]) < 1e-5, (T, rel_l2(yf, yref[:T]))
+            assert np.array_equal(_bits(y), oracle.encode_act(yf, out_dt, "rne")), T
+        gpu.sync()
+    finally:
+        e.free()
