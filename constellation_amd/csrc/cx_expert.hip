@@ -461,8 +461,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 // One expert at 1..4 tokens (single mode), as two launches in which every
 // wave's weights are one round trip of loads.  At this size the launches are
 // bound by per-wave latency and MFMA work, not by HBM: the 16-row x full-K
-// waves of k_gate_up_t<14, 4> / k_down_item take ~10 and ~7 us even with all
-// 44 MB resident in the MALL.
+// waves of k_gate_up_t<14, 4> / k_down_item took 12.7 and 7.1 us at 4 tokens
+// even with all 44 MB resident in the MALL (13.4 and 7.6 from HBM).
 //  * Gate/up (k_gate_up_kpart): 2 k-parts x inter/16 tiles of 8-wave
 //    workgroups (KSA active waves x NKB k-blocks, the shared-expert split of
 //    k_dec_select_sgu), fp32 part sums to L.gu_part[kpart][gate, up][t][row].
