@@ -468,7 +468,12 @@ def main() -> int:
                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": (gu_gbs / HBM_PEAK_GBS) if gu_gbs else None,
                 "algorithmic_bytes_per_launch": gu_bytes, "traffic": measured_traffic(),
-                "traffic_source": TRAFFIC_FILE}
+                "traffic_source": TRAFFIC_FILE,
+                # the whole B=1 layer (router + 9 experts + combine, all launches) on the
+                # same basis: the figure the >= 70 % of HBM peak target is about
+                "layer_achieved": extras["b1"]["layer_gbs"],
+                "layer_frac": extras["b1"]["layer_frac_of_8tbs"],
+                "layer_algorithmic_bytes": extras["b1"]["layer_bytes"]}
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(args.cpu_seconds)

@@ -84,6 +84,7 @@ _SIGS = {
     "cx_layer_destroy": (_I, [_P, _P]),
     "cx_route": (_I, [_P, _P, _I, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.c_float,
                       _P, _P, _P]),
+    "cx_route_logits": (_I, [_P, _P, _I, _I, _P]),
     "cx_moe_decode": (_I, [_P, _P, _P, _I, _I, _P, _P, _I, _P, _I, _P, _P]),
     "cx_moe_prefill": (_I, [_P, _P, _P, _I, _I, _P, _P, _I, _P, _I, _P, _P]),
     "cx_moe_layer": (_I, [_P, _P, _P, _I, _I, _P, _I, _P, _P, _I, _I, _I, _I, C.c_float,

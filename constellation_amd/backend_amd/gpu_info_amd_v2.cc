@@ -15,7 +15,7 @@ bool BuildLocalAmdGpuInfosV2(std::int32_t worker_id_begin, std::uint32_t worker_
     if (out == nullptr) return false;
     out->clear();
     int count = 0;
-    if (cx_device_count(&count) != CX_OK) return true;  // no HIP runtime: no AMD workers
+    if (cx_device_count(&count) != CX_OK) return false;  // as gpu_info_cuda_v2.cc:47-50
     for (int i = 0; i < count; ++i) {
         cx_device_info info;
         if (cx_device_query(i, &info) != CX_OK) continue;
@@ -37,7 +37,7 @@ bool BuildLocalAmdDynamicGpuInfosV2(std::int32_t worker_id_begin,
     if (out == nullptr) return false;
     out->clear();
     int count = 0;
-    if (cx_device_count(&count) != CX_OK) return true;
+    if (cx_device_count(&count) != CX_OK) return false;
     for (int i = 0; i < count; ++i) {
         cx_device_info info;
         if (cx_device_query(i, &info) != CX_OK) continue;

@@ -46,6 +46,25 @@ int set_device(int device) {
     return CX_OK;
 }
 
+// Restores the calling thread's current device when it leaves scope, for
+// entry points that may run on a caller's control thread (device probes,
+// frees) and must not leave another device current there.
+class DeviceRestore {
+public:
+    DeviceRestore() {
+        if (hipGetDevice(&prev_) != hipSuccess) {
+            (void)hipGetLastError();
+            prev_ = -1;
+        }
+    }
+    ~DeviceRestore() {
+        if (prev_ >= 0) (void)hipSetDevice(prev_);
+    }
+
+private:
+    int prev_ = -1;
+};
+
 size_t act_size(int dtype) { return dtype == CX_DTYPE_F32 ? 4 : 2; }
 bool act16(int dtype) { return dtype == CX_DTYPE_FP16 || dtype == CX_DTYPE_BF16; }
 
@@ -123,9 +142,24 @@ int arena_alloc(int device, size_t bytes, void** out) {
     return CX_OK;
 }
 
-int arena_free(int device, void* p) {
+// Returns a range to the free list.  When `in_use` the range may still be read
+// by kernels queued on any stream of the device (a caller frees an expert while
+// its worker thread computes), so the device is synchronised first, as
+// hipFree/cudaFree do: the next upload can then overwrite the range safely.
+int arena_free(int device, void* p, bool in_use = true) {
     if (p == nullptr) return CX_OK;
     Arena& A = arena(device);
+    if (in_use) {
+        {
+            std::lock_guard<std::mutex> lk(A.mu);
+            if (A.live.find(p) == A.live.end())
+                return fail(CX_EINVAL, "cx_free_device: %p not allocated here", p);
+        }
+        DeviceRestore restore;
+        int rc = set_device(device);
+        if (rc) return rc;
+        CX_HIP(hipDeviceSynchronize());
+    }
     std::lock_guard<std::mutex> lk(A.mu);
     auto it = A.live.find(p);
     if (it == A.live.end()) return fail(CX_EINVAL, "cx_free_device: %p not allocated here", p);
@@ -198,6 +232,7 @@ struct cx_ctx {
     int max_lds = 65536;               // dynamic LDS budget per workgroup
     DevBuf plan_buf, hhi, hlo, ypart, logits, route_ids, route_w, hscratch;
     DevBuf gu_part;                    // shared expert's k-part gate/up sums (decode)
+    int route_T = 0, route_E = 0;      // shape of the fp64 logits of the last router call
     DevBuf dx, dy;                     // cx_expert_run_host staging (device)
     void* pin_x = nullptr;             // pinned host staging
     void* pin_y = nullptr;
@@ -234,7 +269,7 @@ class Span {
 public:
     Span(cx_ctx* ctx, const char* name, hipStream_t s) : ctx_(ctx) {
         (void)s;
-        if (!ctx_->prof) return;
+        if (ctx_ == nullptr || !ctx_->prof) return;
         if (hipEventCreate(&t_.start) != hipSuccess || hipEventCreate(&t_.stop) != hipSuccess) {
             (void)hipGetLastError();
             if (t_.start) (void)hipEventDestroy(t_.start);
@@ -338,12 +373,102 @@ int check_desc(const cx_expert_desc* e) {
 
 // Activation rows of one work item that fit the LDS budget next to the
 // reduction tile (<= 16 KB); 0 when staging is not worth it or not possible.
-int lds_rows(const cx_ctx* ctx, int hidden, int max_pairs_per_item) {
+int lds_rows(int max_lds, int hidden, int max_pairs_per_item) {
     if (hidden % 512 != 0) return 0;  // rows are copied in 1 KB wave chunks
-    const int budget = std::min(ctx->max_lds, 65536) - 16384;
+    const int budget = std::min(max_lds, 65536) - 16384;
     const int rows = budget / (hidden * 2 + 16);
     return (max_pairs_per_item <= rows && max_pairs_per_item <= 4) ? max_pairs_per_item : 0;
 }
+
+int lds_rows(const cx_ctx* ctx, int hidden, int max_pairs_per_item) {
+    return lds_rows(ctx->max_lds, hidden, max_pairs_per_item);
+}
+
+// ---------------------------------------------------------------------------
+// One expert over n_tokens tokens (single mode: the tokens are the pairs, the
+// down launch writes the output).  Shared by cx_expert_run (context scratch)
+// and cx_expert_run_static (the library's static device scratch): plan_expert
+// picks the path and states the scratch it needs, run_expert launches it.
+enum ExpertPath { kPathGeneric, kPathSmall, kPathTiles };
+
+struct ExpertPlan {
+    ExpertLaunch L;
+    int path;
+    size_t h_f32_bytes;   // generic path: fp32 h [T, I]
+    size_t h_plane_bytes; // tile path: each bf16 plane h_hi / h_lo [T, I]
+    size_t gu_part_bytes; // small path: k-part gate/up sums [2][2][T][I] fp32
+};
+
+ExpertPlan plan_expert(const cx_expert_desc& e, const void* x, int in_dtype, int n_tokens,
+                       void* y, int out_dtype, float* y_f32, int max_lds) {
+    ExpertPlan P{};
+    const size_t TI = (size_t)n_tokens * e.inter;
+    if (!fast_path_ok(e)) {
+        P.path = kPathGeneric;
+        P.h_f32_bytes = TI * 4;
+        return P;
+    }
+    ExpertLaunch& L = P.L;
+    L.table = nullptr;
+    L.single = e;
+    L.n_tokens = n_tokens;
+    L.hidden = e.hidden;
+    L.inter = e.inter;
+    L.maxt = n_tokens <= kTileTok ? 1 : 4;
+    L.x = x;
+    L.in_dtype = in_dtype;
+    L.y = y;
+    L.y_f32 = y_f32;
+    L.out_dtype = out_dtype;
+    L.np_lds = L.maxt == 1 ? lds_rows(max_lds, e.hidden, n_tokens) : 0;
+    L.max_lds = max_lds;
+    if (expert_small_ok(L)) {
+        P.path = kPathSmall;
+        P.gu_part_bytes = sizeof(float) * 2 * 2 * TI;
+        L.gu_kparts = 2;
+    } else {
+        P.path = kPathTiles;
+        P.h_plane_bytes = TI * 2;
+    }
+    return P;
+}
+
+// Launches a planned expert on `s`; the scratch pointers the path needs are
+// set (h_f32 / h_hi + h_lo / gu_part).  ctx (nullable) only collects timing.
+int run_expert(cx_ctx* ctx, ExpertPlan& P, const cx_expert_desc& e, const void* x, int in_dtype,
+               int n_tokens, void* y, int out_dtype, float* y_f32, float* h_f32, uint16_t* h_hi,
+               uint16_t* h_lo, float* gu_part, hipStream_t s) {
+    if (P.path == kPathGeneric) {
+        CX_HIP(launch_generic_expert(e, x, in_dtype, n_tokens, h_f32, y, out_dtype, y_f32, s));
+        return CX_OK;
+    }
+    ExpertLaunch& L = P.L;
+    if (P.path == kPathSmall) {
+        L.gu_part = gu_part;
+        {
+            Span sp(ctx, "gate_up", s);
+            CX_HIP(launch_gate_up_kpart(L, s));
+        }
+        Span sp(ctx, "down", s);
+        CX_HIP(launch_down_ks(L, s));
+        return CX_OK;
+    }
+    L.h_hi = h_hi;
+    L.h_lo = h_lo;
+    {
+        Span sp(ctx, "gate_up", s);
+        CX_HIP(launch_gate_up(L, s));
+    }
+    {
+        Span sp(ctx, "down", s);
+        CX_HIP(launch_down(L, s));
+    }
+    return CX_OK;
+}
+
+}  // namespace
+
+namespace {
 
 // The decode pipeline (T <= 16) serves this layer / router shape.
 bool dec_path_ok(const cx_layer* layer, int top_k, const RouteArgs* route) {
@@ -550,6 +675,8 @@ int fill_route(cx_ctx* ctx, const void* x, int x_dtype, const void* w_router, in
     int rc = set_device(ctx->device);
     if (rc) return rc;
     if ((rc = ensure(&ctx->logits, (size_t)n_tokens * n_experts * 8, s))) return rc;
+    ctx->route_T = n_tokens;
+    ctx->route_E = n_experts;
     *R = RouteArgs{};
     R->x = x;
     R->x_dtype = x_dtype;
@@ -676,6 +803,7 @@ int cx_device_count(int* count) {
 int cx_device_query(int device, cx_device_info* out) {
     if (!out) return fail(CX_EINVAL, "NULL out");
     std::memset(out, 0, sizeof(*out));
+    DeviceRestore restore;  // the node probes from its control thread
     int rc = set_device(device);
     if (rc) return rc;
     hipDeviceProp_t prop;
@@ -714,7 +842,7 @@ int cx_upload_matrix(int device, const uint8_t* host_weight, uint64_t rows, uint
     void *pw = nullptr, *ps = nullptr;
     if ((rc = arena_alloc(device, wbytes, &pw))) return rc;
     if ((rc = arena_alloc(device, sbytes, &ps))) {
-        arena_free(device, pw);
+        arena_free(device, pw, false);
         return rc;
     }
     hipStream_t s = upload_stream(device);
@@ -723,8 +851,8 @@ int cx_upload_matrix(int device, const uint8_t* host_weight, uint64_t rows, uint
     if (e == hipSuccess) e = launch_canonicalize_fp8(static_cast<uint8_t*>(pw), wbytes, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
-        arena_free(device, pw);
-        arena_free(device, ps);
+        arena_free(device, pw, false);
+        arena_free(device, ps, false);
         return fail(CX_EHIP, "upload failed: %s", hipGetErrorString(e));
     }
     *dev_weight = static_cast<uint8_t*>(pw);
@@ -809,10 +937,11 @@ int cx_ctx_sync(cx_ctx* ctx, void* stream) {
     if (flag != 0) {
         CX_HIP(hipMemsetAsync(ctx->err_flag, 0, sizeof(int), s));
         CX_HIP(hipStreamSynchronize(s));
-        return fail(CX_EDEVICE, "device check failed (flags 0x%x:%s%s%s)", flag,
+        return fail(CX_EDEVICE, "device check failed (flags 0x%x:%s%s%s%s)", flag,
                     (flag & kErrBadExpertId) ? " expert id out of range" : "",
                     (flag & kErrNotResident) ? " expert not resident" : "",
-                    (flag & kErrPlanOverflow) ? " plan overflow" : "");
+                    (flag & kErrPlanOverflow) ? " plan overflow" : "",
+                    (flag & kErrDuplicateRoute) ? " expert routed twice for one token" : "");
     }
     return CX_OK;
 }
@@ -847,52 +976,15 @@ int cx_expert_run(cx_ctx* ctx, const cx_expert_desc* expert, const void* x, int 
     if (n_tokens <= 0 || !x || !y) return fail(CX_EINVAL, "bad n_tokens or NULL buffer");
     if ((rc = set_device(ctx->device))) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const size_t I = expert->inter;
-    if (!fast_path_ok(*expert)) {
-        if ((rc = ensure(&ctx->hscratch, (size_t)n_tokens * I * 4, s))) return rc;
-        CX_HIP(launch_generic_expert(*expert, x, in_dtype, n_tokens,
-                                     static_cast<float*>(ctx->hscratch.p), y, out_dtype, y_f32, s));
-        return CX_OK;
-    }
-    if ((rc = ensure(&ctx->hhi, (size_t)n_tokens * I * 2, s))) return rc;
-    if ((rc = ensure(&ctx->hlo, (size_t)n_tokens * I * 2, s))) return rc;
-    ExpertLaunch L{};
-    L.table = nullptr;
-    L.single = *expert;
-    L.n_tokens = n_tokens;
-    L.hidden = expert->hidden;
-    L.inter = expert->inter;
-    L.maxt = n_tokens <= kTileTok ? 1 : 4;
-    L.x = x;
-    L.in_dtype = in_dtype;
-    L.h_hi = static_cast<uint16_t*>(ctx->hhi.p);
-    L.h_lo = static_cast<uint16_t*>(ctx->hlo.p);
-    L.y = y;
-    L.y_f32 = y_f32;
-    L.out_dtype = out_dtype;
-    L.np_lds = L.maxt == 1 ? lds_rows(ctx, expert->hidden, n_tokens) : 0;
-    L.max_lds = ctx->max_lds;
-    if (expert_small_ok(L)) {
-        if ((rc = ensure(&ctx->gu_part, sizeof(float) * 2 * 2 * (size_t)n_tokens * I, s))) return rc;
-        L.gu_part = static_cast<float*>(ctx->gu_part.p);
-        L.gu_kparts = 2;
-        {
-            Span sp(ctx, "gate_up", s);
-            CX_HIP(launch_gate_up_kpart(L, s));
-        }
-        Span sp(ctx, "down", s);
-        CX_HIP(launch_down_ks(L, s));
-        return CX_OK;
-    }
-    {
-        Span sp(ctx, "gate_up", s);
-        CX_HIP(launch_gate_up(L, s));
-    }
-    {
-        Span sp(ctx, "down", s);
-        CX_HIP(launch_down(L, s));
-    }
-    return CX_OK;
+    ExpertPlan P = plan_expert(*expert, x, in_dtype, n_tokens, y, out_dtype, y_f32, ctx->max_lds);
+    if (P.h_f32_bytes && (rc = ensure(&ctx->hscratch, P.h_f32_bytes, s))) return rc;
+    if (P.h_plane_bytes && ((rc = ensure(&ctx->hhi, P.h_plane_bytes, s)) ||
+                            (rc = ensure(&ctx->hlo, P.h_plane_bytes, s))))
+        return rc;
+    if (P.gu_part_bytes && (rc = ensure(&ctx->gu_part, P.gu_part_bytes, s))) return rc;
+    return run_expert(ctx, P, *expert, x, in_dtype, n_tokens, y, out_dtype, y_f32,
+                      static_cast<float*>(ctx->hscratch.p), static_cast<uint16_t*>(ctx->hhi.p),
+                      static_cast<uint16_t*>(ctx->hlo.p), static_cast<float*>(ctx->gu_part.p), s);
 }
 
 int cx_expert_run_host(cx_ctx* ctx, const cx_expert_desc* expert, const void* x_host,
@@ -1008,6 +1100,18 @@ int cx_route(cx_ctx* ctx, const void* x, int x_dtype, const void* w_router, int 
     return CX_OK;
 }
 
+int cx_route_logits(cx_ctx* ctx, double* out, int n_tokens, int n_experts, void* stream) {
+    if (!ctx || !out) return fail(CX_EINVAL, "NULL argument");
+    if (ctx->route_T == 0 || n_tokens != ctx->route_T || n_experts != ctx->route_E)
+        return fail(CX_EINVAL, "no router logits of shape [%d, %d] (last router call: [%d, %d])",
+                    n_tokens, n_experts, ctx->route_T, ctx->route_E);
+    int rc = set_device(ctx->device);
+    if (rc) return rc;
+    CX_HIP(hipMemcpyAsync(out, ctx->logits.p, (size_t)n_tokens * n_experts * sizeof(double),
+                          hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream)));
+    return CX_OK;
+}
+
 int cx_moe_decode(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int n_tokens,
                   const int32_t* topk_ids, const float* topk_w, int top_k, void* y, int out_dtype,
                   float* y_f32, void* stream) {
@@ -1084,14 +1188,21 @@ int cx_moe_layer_request_run(cx_ctx* ctx, const cx_layer* layer, const uint8_t* 
     // request-level checks, mapped to the worker's status codes
     int status = 0;
     bool any_route = false;
+    bool bad_weight = false;
     for (size_t i = 0; i < r.n_routes && status != 1; ++i) {
         int32_t id;
+        float wt;
         std::memcpy(&id, r.ids + 4 * i, 4);
+        std::memcpy(&wt, r.w + 4 * i, 4);
         if (id < 0) continue;
         any_route = true;
+        // validate_routes (server/moe_layer_runtime.py:96-97) rejects negative
+        // weights; a non-finite one cannot be combined either
+        if (!(wt >= 0.0f) || wt > 3.4028234663852886e38f) bad_weight = true;
         if (id >= layer->n_experts) status = 1;
         else if (!layer->resident[id] && status == 0) status = 2;
     }
+    if (status == 0 && bad_weight) status = 4;
     const bool want_shared = (h.flags & CX_MOE_LAYER_FLAG_SHARED) != 0;
     if (status == 0 && want_shared && !layer->has_shared) status = 2;
     if (status == 0 && (H != layer->hidden || !layer->fast)) status = 4;
@@ -1183,7 +1294,7 @@ int cx_gen_expert(int device, uint64_t seed, uint64_t stream_base, int hidden, i
                           (size_t)hidden * inter, nsd * 4};
     for (int i = 0; i < 6; ++i) {
         if ((rc = arena_alloc(device, sz[i], &p[i]))) {
-            for (int j = 0; j < i; ++j) arena_free(device, p[j]);
+            for (int j = 0; j < i; ++j) arena_free(device, p[j], false);
             return rc;
         }
     }
@@ -1198,7 +1309,7 @@ int cx_gen_expert(int device, uint64_t seed, uint64_t stream_base, int hidden, i
                            static_cast<uint8_t*>(p[4]), static_cast<float*>(p[5]), s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
-        for (int j = 0; j < 6; ++j) arena_free(device, p[j]);
+        for (int j = 0; j < 6; ++j) arena_free(device, p[j], false);
         return fail(CX_EHIP, "expert generation failed: %s", hipGetErrorString(e));
     }
     out->w_up = static_cast<uint8_t*>(p[0]);

@@ -241,6 +241,13 @@ class Context:
                              ids.data_ptr(), w.data_ptr(), self.stream()))
         return ids, w
 
+    def route_logits(self, n_tokens: int, n_experts: int, device) -> torch.Tensor:
+        """fp64 router logits [n_tokens, n_experts] of the last route call."""
+        out = torch.empty((n_tokens, n_experts), dtype=torch.float64, device=device)
+        check(lib().cx_route_logits(self.handle, out.data_ptr(), n_tokens, n_experts,
+                                    self.stream()))
+        return out
+
     # -- grouped MoE -----------------------------------------------------------
     def moe(self, layer: Layer, x: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Tensor, *,
             out_dtype: Optional[torch.dtype] = None, want_f32: bool = False,

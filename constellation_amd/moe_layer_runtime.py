@@ -15,12 +15,17 @@ Differences from the reference, by design:
   * `hidden` may also be fp16/bf16 and `gate_weight` bf16 (the checkpoint's
     own dtype): the products are exact in fp64 either way, so the decision
     is the same as for their fp32 casts.  fp32 inputs, as the reference
-    requires, are accepted unchanged.
+    requires, are accepted unchanged; fp16 `hidden` is widened to fp32
+    (exactly) before the router, which reads bf16 or fp32.
   * the returned order is descending score (the reference's
     `topk(sorted=False)` order is unspecified).
-  * `return_aux=True` returns the decision-side fields only (indices,
-    weights, masks, effective_top_k, routes); the intermediate score
-    vectors are not materialised by the fused kernels.
+  * `return_aux=True` returns the reference's aux keys
+    (moe_layer_runtime.py:386-407).  They are derived on the host from the
+    router kernel's own fp64 logits (cx_route_logits) in float64 and
+    returned as float32 / int64 / bool numpy arrays like the reference's,
+    so `selected_group_idx`, `group_mask`, `score_mask` and
+    `topk_choice_vals` describe the decision the kernel made; `topk_idx`
+    and `topk_weight` are the kernel's outputs themselves.
 
 `route_tokens` is the batched form ([T, hidden] in, device tensors out) for
 prefill chunks and batched decode.
@@ -150,7 +155,7 @@ def route_tokens(hidden, gate_weight, e_score_correction_bias, *, n_group: int, 
     mask = _resident_mask(resident_expert_ids, num_experts, gate_weight.device)
     ctx = _context(dev)
     with torch.cuda.device(dev):
-        ids, w = ctx.route(hidden, gate_weight, e_score_correction_bias, resident=mask,
+        ids, w = ctx.route(_router_input(hidden), gate_weight, e_score_correction_bias, resident=mask,
                            n_group=n_group, topk_group=topk_group, top_k=top_k,
                            norm_topk_prob=bool(norm_topk_prob),
                            routed_scaling_factor=float(routed_scaling_factor))
@@ -172,22 +177,74 @@ def route_token_real(hidden, gate_weight: torch.Tensor, e_score_correction_bias:
     mask = _resident_mask(resident_expert_ids, num_experts, gate_weight.device)
     ctx = _context(dev)
     with torch.cuda.device(dev):
-        ids, w = ctx.route(hidden.view(1, -1), gate_weight, e_score_correction_bias, resident=mask,
-                           n_group=n_group, topk_group=topk_group, top_k=top_k,
+        ids, w = ctx.route(_router_input(hidden).view(1, -1), gate_weight, e_score_correction_bias,
+                           resident=mask, n_group=n_group, topk_group=topk_group, top_k=top_k,
                            norm_topk_prob=bool(norm_topk_prob),
                            routed_scaling_factor=float(routed_scaling_factor))
+        logits = ctx.route_logits(1, num_experts, gate_weight.device) if return_aux else None
         ctx.sync()
     ids_l = ids[0].tolist()
     w_l = w[0].tolist()
     routes = [(int(e), float(x)) for e, x in zip(ids_l, w_l) if e >= 0]
     if not return_aux:
         return routes
-    n_res = num_experts if mask is None else int(mask.sum().item())
-    aux = {
-        "topk_idx": [e for e, _ in routes],
-        "topk_weight": [x for _, x in routes],
-        "resident_mask": None if mask is None else mask.bool().cpu().numpy(),
-        "effective_top_k": min(top_k, n_res),
+    aux = _route_aux(logits[0].cpu().numpy(), e_score_correction_bias.detach().cpu().numpy(),
+                     None if mask is None else mask.cpu().numpy().astype(bool),
+                     n_group=n_group, topk_group=topk_group, norm_topk_prob=bool(norm_topk_prob),
+                     routes=routes)
+    return routes, aux
+
+
+def _router_input(hidden: torch.Tensor) -> torch.Tensor:
+    """The router kernel reads bf16 or fp32 activations; fp16 widens exactly."""
+    return hidden.float() if hidden.dtype == torch.float16 else hidden
+
+
+def _route_aux(logits64, bias, resident, *, n_group: int, topk_group: int,
+               norm_topk_prob: bool, routes):
+    """The reference's aux dict (server/moe_layer_runtime.py:321-407), from
+    the kernel's fp64 logits of one token, in the reference's step order,
+    evaluated in float64 on the host (diagnostics only: the routes come from
+    the kernel).  Ranking ties go to the lower index, as in the kernel."""
+    import numpy as np
+
+    E = logits64.shape[0]
+    epg = E // n_group
+    lg = np.asarray(logits64, np.float64)
+    s_raw = 1.0 / (1.0 + np.exp(-lg))
+    c_raw = s_raw + np.asarray(bias, np.float64)
+    res = np.ones(E, bool) if resident is None else np.asarray(resident, bool)
+    c = np.where(res, c_raw, -np.inf)
+    s = np.where(res, s_raw, 0.0)
+    grouped = c.reshape(n_group, epg)
+    top2 = -np.sort(-grouped, axis=1, kind="stable")[:, :2]
+    group_scores = top2.sum(axis=1)
+    order = np.lexsort((np.arange(n_group), -group_scores))  # descending, lower index first
+    sel = np.sort(order[:topk_group]).astype(np.int64)
+    group_mask = np.zeros(n_group, bool)
+    group_mask[sel] = True
+    score_mask = np.repeat(group_mask, epg)
+    idx = np.asarray([e for e, _ in routes], np.int64)
+    k = int(idx.size)
+    pre = s[idx]
+    post = pre / (pre.sum() + 1e-20) if (norm_topk_prob and k > 1) else pre.copy()
+    f32 = np.float32
+    return {
+        "logits": lg.astype(f32),
+        "scores_raw": s_raw.astype(f32),
+        "scores": s.astype(f32),
+        "scores_for_choice_raw": c_raw.astype(f32),
+        "scores_for_choice": c.astype(f32),
+        "group_scores": group_scores.astype(f32),
+        "selected_group_idx": sel,
+        "group_mask": group_mask,
+        "score_mask": score_mask,
+        "resident_mask": res,
+        "topk_idx": idx,
+        "topk_choice_vals": c[idx].astype(f32),
+        "topk_weight_pre_norm": pre.astype(f32),
+        "topk_weight_post_norm": post.astype(f32),
+        "topk_weight": np.asarray([x for _, x in routes], f32),
+        "effective_top_k": k,
         "routes": routes,
     }
-    return routes, aux

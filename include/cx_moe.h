@@ -90,7 +90,10 @@ CX_API int cx_upload_matrix(int device,
 
 /* Release one arena sub-allocation made by this library (weight or scale).
  * device < 0 searches every device's arena for the pointer (the reference's
- * FreeDeviceBuffer takes no device either).  NULL is a no-op.
+ * FreeDeviceBuffer takes no device either).  NULL is a no-op.  Like
+ * cudaFree, it first waits for all work queued on the device, so kernels
+ * still reading the range (another thread's inference) finish before a later
+ * upload can reuse it; the calling thread's current device is left as it was.
  * Replaces FreeDeviceBuffer (backend/cuda/backend_cuda_v2.cc:55-65). */
 CX_API int cx_free_device(int device, void* dev_ptr);
 
@@ -184,6 +187,15 @@ CX_API int cx_route(cx_ctx* ctx, const void* x, int x_dtype,
              float routed_scaling_factor, int32_t* topk_ids, float* topk_w,
              void* stream);
 
+/* Copies the fp64 router logits W_r . x [n_tokens, n_experts] of the
+ * context's most recent router call (cx_route or cx_moe_layer) into `out`
+ * (device memory), ordered on `stream` after that call.  For the diagnostic
+ * fields route_token_real returns with return_aux=True (logits, scores,
+ * group scores; server/moe_layer_runtime.py:386-407).  CX_EINVAL when the
+ * shape differs from the last call's. */
+CX_API int cx_route_logits(cx_ctx* ctx, double* out, int n_tokens, int n_experts,
+                    void* stream);
+
 /* Routed-expert compute for a token batch: every active expert and the
  * shared expert of the layer in grouped launches, with per-expert token
  * gather and a deterministic weighted combine (fp32, route order, shared
@@ -191,7 +203,9 @@ CX_API int cx_route(cx_ctx* ctx, const void* x, int x_dtype,
  * (moe_layer_runtime.py:111-167, deepseek_full_model_executor.py:264-316,
  * full_model_runtime.py:348).  Negative ids are skipped; an id that is out
  * of range or not resident sets the context's device error (reported by
- * cx_ctx_sync) and is skipped.
+ * cx_ctx_sync) and is skipped.  Route weights are used as given (the
+ * device-pointer entry points do not inspect them; the wire entry point
+ * cx_moe_layer_request_run rejects negative and non-finite ones).
  * cx_moe_decode targets n_tokens <= 16 per launch set;
  * cx_moe_prefill targets larger chunks (grouped MFMA GEMM tiles of 16
  * tokens, up to 64 tokens per work item).  Both accept any n_tokens. */
@@ -256,7 +270,9 @@ CX_API size_t cx_moe_layer_response_size(int batch_size, int hidden_dim);
  * cx_moe_prefill, one device->host copy.  Writes the response body into
  * resp[resp_cap] (resp_cap >= cx_moe_layer_response_size) and its length
  * into *resp_len.  Request-level failures (unknown / non-resident expert,
- * hidden mismatch, a device check) become a status code in the response
+ * hidden mismatch, a negative or non-finite route weight — rejected like
+ * validate_routes, server/moe_layer_runtime.py:96-97 — or a device check)
+ * become a status code in the response
  * and CX_OK; a malformed body or an undersized buffer returns CX_EINVAL
  * without a response. */
 CX_API int cx_moe_layer_request_run(cx_ctx* ctx, const cx_layer* layer,

@@ -307,3 +307,31 @@ def test_small_batch_expert_small_dims(gpu, oracle, H, in_dt, out_dt):
         gpu.sync()
     finally:
         e.free()
+
+
+def test_free_waits_for_queued_work_before_reuse(gpu):
+    """cx_free_device behaves like cudaFree (backend_cuda_v2.cc:55-65): kernels
+    queued on another stream that still read the freed expert finish before
+    the next upload (on the library's own upload stream) reuses its range."""
+    from constellation_amd.engine import Expert
+    print("[arena] free while queued kernels read the expert", flush=True)
+    a = Expert.generate(0, 91, 0x910)
+    x = gpu.gen_normal(91, 0x91F, (16, 7168), 1.0, torch.bfloat16)
+    y_ref = gpu.expert_run(a, x)
+    torch.cuda.synchronize()
+    outs = [gpu.expert_run(a, x) for _ in range(24)]  # queued, not waited for
+    a_ptrs = (a.desc.w_up, a.desc.w_gate, a.desc.w_down)
+    a.free()
+    rng = np.random.default_rng(91)
+    H, I = 7168, 2048
+    b = Expert.upload(0, rng.integers(0, 0x7E, (I, H), dtype=np.uint8), np.ones((16, 56), np.float32),
+                      rng.integers(0, 0x7E, (I, H), dtype=np.uint8), np.ones((16, 56), np.float32),
+                      rng.integers(0, 0x7E, (H, I), dtype=np.uint8), np.ones((56, 16), np.float32))
+    try:
+        reused = (b.desc.w_up, b.desc.w_gate, b.desc.w_down) == a_ptrs
+        print(f"[arena] range reused: {reused}", flush=True)
+        torch.cuda.synchronize()
+        for y in outs:
+            assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+    finally:
+        b.free()

@@ -616,12 +616,14 @@ def test_moe_layer_request_status_codes(gpu, oracle):
         x = gpu.gen_normal(1, 1, (2, H), 1.0, torch.bfloat16)
         act = x.cpu().view(torch.int16).numpy().tobytes()
 
-        def run(ids, flags=0):
+        def run(ids, flags=0, wts=None):
             ids = np.asarray(ids, np.int32)
+            if wts is None:
+                wts = np.full(ids.shape, 0.5, np.float32)
             body = P.encode_moe_layer_request({
                 "layer_id": 0, "batch_size": 2, "hidden_dim": H, "top_k": ids.shape[1],
                 "input_dtype": BF16, "output_dtype": BF16, "flags": flags, "expert_ids": ids,
-                "expert_weights": np.full(ids.shape, 0.5, np.float32), "activation": act})
+                "expert_weights": np.asarray(wts, np.float32), "activation": act})
             return P.decode_moe_layer_response(gpu.moe_layer_request(layer, body))
 
         ok = run([[0, -1], [0, -1]])
@@ -630,6 +632,12 @@ def test_moe_layer_request_status_codes(gpu, oracle):
                                  ([[0, -1], [0, -1]], P.FLAG_SHARED, 2), ([[0, 0], [0, -1]], 0, 4)):
             r = run(ids, flags)
             assert r["status_code"] == code and r["output"] == b"", (ids, flags, r["status_code"])
+        # validate_routes (server/moe_layer_runtime.py:96-97): a negative weight is
+        # refused; so is a non-finite one.  The weight of an absent route (-1) is unused.
+        for bad in (-0.25, float("nan"), float("inf")):
+            r = run([[0, -1], [0, -1]], wts=[[bad, 0.5], [0.5, 0.5]])
+            assert r["status_code"] == 4 and r["output"] == b"", bad
+        assert run([[0, -1], [0, -1]], wts=[[0.5, -1.0], [0.5, float("nan")]]) == ok
         again = run([[0, -1], [0, -1]])  # a failure leaves the context usable
         assert again == ok
     finally:
