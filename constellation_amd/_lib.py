@@ -19,6 +19,8 @@ CX_EHIP = -3
 CX_EUNSUPPORTED = -4
 CX_EDEVICE = -5
 
+CX_STATIC_SCRATCH_BYTES = 256 * 1024  # include/cx_moe.h
+
 FP16, BF16, F32 = 1, 2, 3
 
 
@@ -77,6 +79,7 @@ _SIGS = {
     "cx_ctx_profile": (_I, [_P, _I]),
     "cx_ctx_profile_read": (_I, [_P, C.c_char_p, C.POINTER(_I), C.POINTER(C.c_double)]),
     "cx_expert_run": (_I, [_P, C.POINTER(ExpertDesc), _P, _I, _I, _P, _I, _P, _P]),
+    "cx_expert_run_static": (_I, [_I, C.POINTER(ExpertDesc), _P, _I, _I, _P, _I, _P, _P]),
     "cx_expert_run_host": (_I, [_P, C.POINTER(ExpertDesc), _P, C.c_size_t, _I, _I, _P,
                                 C.c_size_t, _I]),
     "cx_layer_create": (_I, [_P, _I, C.POINTER(C.POINTER(ExpertDesc)), C.POINTER(ExpertDesc),

@@ -466,6 +466,45 @@ int run_expert(cx_ctx* ctx, ExpertPlan& P, const cx_expert_desc& e, const void* 
     return CX_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of cx_expert_run_static: a file-scope device array.  Every GPU the
+// library runs on holds its own copy, at its own address, until the process
+// ends.  In host code `scratch` names a host-side stand-in, never device
+// memory: static_scratch() looks up the device address once per device (with
+// that device current) and every kernel argument uses that address.
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[CX_STATIC_SCRATCH_BYTES];
+
+std::mutex g_static_mu;
+unsigned char* g_static_ptr[kMaxDevices] = {};
+int g_static_lds[kMaxDevices] = {};
+
+// The calling thread's current device must be `device`.
+int static_scratch(int device, unsigned char** ptr, int* max_lds) {
+    std::lock_guard<std::mutex> lk(g_static_mu);
+    if (g_static_ptr[device] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            (void)hipGetLastError();
+            return fail(CX_EHIP, "hipGetSymbolAddress(scratch) on device %d failed: %s", device,
+                        hipGetErrorString(e));
+        }
+        int lds = 0;
+        if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) !=
+                hipSuccess ||
+            lds <= 0) {
+            (void)hipGetLastError();
+            lds = 65536;
+        }
+        g_static_lds[device] = lds;
+        g_static_ptr[device] = static_cast<unsigned char*>(p);
+    }
+    *ptr = g_static_ptr[device];
+    *max_lds = g_static_lds[device];
+    return CX_OK;
+}
+
 }  // namespace
 
 namespace {
@@ -985,6 +1024,32 @@ int cx_expert_run(cx_ctx* ctx, const cx_expert_desc* expert, const void* x, int 
     return run_expert(ctx, P, *expert, x, in_dtype, n_tokens, y, out_dtype, y_f32,
                       static_cast<float*>(ctx->hscratch.p), static_cast<uint16_t*>(ctx->hhi.p),
                       static_cast<uint16_t*>(ctx->hlo.p), static_cast<float*>(ctx->gu_part.p), s);
+}
+
+int cx_expert_run_static(int device, const cx_expert_desc* expert, const void* x, int in_dtype,
+                         int n_tokens, void* y, int out_dtype, float* y_f32, void* stream) {
+    int rc = check_desc(expert);
+    if (rc) return rc;
+    if (!act16(in_dtype) || !act16(out_dtype)) return fail(CX_EINVAL, "dtypes must be fp16/bf16");
+    if (n_tokens <= 0 || !x || !y) return fail(CX_EINVAL, "bad n_tokens or NULL buffer");
+    if (device < 0 || device >= kMaxDevices) return fail(CX_EINVAL, "invalid device %d", device);
+    if ((rc = set_device(device))) return rc;
+    unsigned char* base = nullptr;
+    int max_lds = 0;
+    if ((rc = static_scratch(device, &base, &max_lds))) return rc;
+    ExpertPlan P = plan_expert(*expert, x, in_dtype, n_tokens, y, out_dtype, y_f32, max_lds);
+    // one region per path: fp32 h, or h_hi then h_lo (256-B aligned), or the part sums
+    const size_t lo_off = (P.h_plane_bytes + 255) & ~(size_t)255;
+    const size_t need = std::max({P.h_f32_bytes, lo_off + P.h_plane_bytes, P.gu_part_bytes});
+    if (need > CX_STATIC_SCRATCH_BYTES)
+        return fail(CX_EINVAL,
+                    "cx_expert_run_static: %d tokens x inter %d need %zu scratch bytes, "
+                    "more than the static %d (use cx_expert_run)",
+                    n_tokens, expert->inter, need, (int)CX_STATIC_SCRATCH_BYTES);
+    return run_expert(nullptr, P, *expert, x, in_dtype, n_tokens, y, out_dtype, y_f32,
+                      reinterpret_cast<float*>(base), reinterpret_cast<uint16_t*>(base),
+                      reinterpret_cast<uint16_t*>(base + lo_off), reinterpret_cast<float*>(base),
+                      static_cast<hipStream_t>(stream));
 }
 
 int cx_expert_run_host(cx_ctx* ctx, const cx_expert_desc* expert, const void* x_host,

@@ -143,6 +143,25 @@ CX_API int cx_expert_run(cx_ctx* ctx, const cx_expert_desc* expert,
                   const void* x, int in_dtype, int n_tokens,
                   void* y, int out_dtype, float* y_f32, void* stream);
 
+/* Allocation-free variant of cx_expert_run.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory — code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  It takes no
+ * context and never calls hipMalloc, hipFree or an allocating library
+ * routine; its scratch (h, or the k-part gate/up sums at 1..4 tokens) is a
+ * static device array of CX_STATIC_SCRATCH_BYTES that each GPU holds until the
+ * process ends.  Same kernels and results as cx_expert_run.
+ * Limit: the path's scratch must fit in CX_STATIC_SCRATCH_BYTES — 16 bytes
+ * per (token, inter row) at 1..4 tokens, 4 bytes (plus up to 256 of
+ * alignment) otherwise; at DeepSeek-V3's inter 2048 that is up to 32 tokens.
+ * A larger call returns CX_EINVAL.  Every call on one GPU shares that GPU's
+ * array, so calls that overlap on one GPU (two streams, two threads) race;
+ * serialise them.  Nothing in the array has to start at zero: each call
+ * writes what it reads. */
+#define CX_STATIC_SCRATCH_BYTES (256 * 1024)
+CX_API int cx_expert_run_static(int device, const cx_expert_desc* expert,
+                         const void* x, int in_dtype, int n_tokens,
+                         void* y, int out_dtype, float* y_f32, void* stream);
+
 /* Host-buffer variant with the exact contract of
  * BackendWorkspaceV2::RunExpertRequest (backend/backend_workspace_v2.h:18-21)
  * as implemented for CUDA at backend_workspace_cuda_v2.cc:26-109/139-182:
