@@ -849,6 +849,12 @@ int cx_device_query(int device, cx_device_info* out) {
     CX_HIP(hipGetDeviceProperties(&prop, device));
     std::snprintf(out->name, sizeof(out->name), "%s", prop.name);
     std::snprintf(out->arch, sizeof(out->arch), "%s", prop.gcnArchName);
+    if (out->name[0] == '\0') {
+        // the marketing name comes from libdrm's amdgpu.ids, which a host may
+        // lack: name the device by its architecture instead
+        const size_t n = std::strcspn(prop.gcnArchName, ":");
+        std::snprintf(out->name, sizeof(out->name), "AMD %.*s", static_cast<int>(n), prop.gcnArchName);
+    }
     out->total_mem_bytes = prop.totalGlobalMem;
     size_t fr = 0, tot = 0;
     CX_HIP(hipMemGetInfo(&fr, &tot));

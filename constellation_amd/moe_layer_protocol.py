@@ -13,20 +13,107 @@ the node by cx_moe_layer_request_run.
 """
 from __future__ import annotations
 
+import socket
 import struct
 
 import numpy as np
 
+# v1 framing (common/protocol.h:10-62): every message is a 16-byte little-endian
+# header (magic "EXPT", version 1, msg_type, request_id, body_len) + body.
+MAGIC = 0x45585054
+VERSION = 1
+INFER_REQUEST = 40
+INFER_RESPONSE = 41
 MOE_LAYER_REQUEST = 42
 MOE_LAYER_RESPONSE = 43
 FLAG_SHARED = 1
+HEADER_BYTES = 16
 
+_HDR = struct.Struct("<IHHII")
 _I32 = struct.Struct("<i")
 _U32 = struct.Struct("<I")
 
 
 class ProtocolError(ValueError):
     pass
+
+
+def encode_header(msg_type: int, request_id: int, body_len: int) -> bytes:
+    return _HDR.pack(MAGIC, VERSION, int(msg_type), int(request_id) & 0xFFFFFFFF, int(body_len))
+
+
+def decode_header(b: bytes) -> dict:
+    """Header fields; a wrong magic or version is a ProtocolError, as the worker
+    loop closes the connection on them (expert_node_v2/worker.cc:219-235)."""
+    if len(b) != HEADER_BYTES:
+        raise ProtocolError(f"header must be {HEADER_BYTES} bytes, got {len(b)}")
+    magic, version, msg_type, rid, n = _HDR.unpack(b)
+    if magic != MAGIC:
+        raise ProtocolError(f"bad magic 0x{magic:x}")
+    if version != VERSION:
+        raise ProtocolError(f"bad version {version}")
+    return {"magic": magic, "version": version, "msg_type": msg_type, "request_id": rid,
+            "body_len": n}
+
+
+def frame(msg_type: int, request_id: int, body: bytes) -> bytes:
+    """Header + body, ready for one sendall."""
+    return encode_header(msg_type, request_id, len(body)) + bytes(body)
+
+
+def _recv_exact(sock: socket.socket, n: int) -> bytes:
+    buf = bytearray()
+    while len(buf) < n:
+        chunk = sock.recv(n - len(buf))
+        if not chunk:
+            raise ConnectionError(f"connection closed after {len(buf)} of {n} bytes")
+        buf += chunk
+    return bytes(buf)
+
+
+def recv_frame(sock: socket.socket) -> tuple[dict, bytes]:
+    """Reads one framed message: (header fields, body)."""
+    hdr = decode_header(_recv_exact(sock, HEADER_BYTES))
+    return hdr, _recv_exact(sock, hdr["body_len"])
+
+
+def request(sock: socket.socket, msg_type: int, request_id: int, body: bytes,
+            expect_type: int) -> bytes:
+    """Sends one framed request on a connected socket and returns the reply body
+    (checking its type and request_id)."""
+    sock.sendall(frame(msg_type, request_id, body))
+    hdr, reply = recv_frame(sock)
+    if hdr["msg_type"] != expect_type or hdr["request_id"] != (int(request_id) & 0xFFFFFFFF):
+        raise ProtocolError(f"unexpected reply type={hdr['msg_type']} rid={hdr['request_id']}")
+    return reply
+
+
+# -- v1 InferRequest / InferResponse (common/infer_codec.cc:7-76; byte-identical) --
+
+def encode_infer_request(msg) -> bytes:
+    act = msg["activation"]
+    if not isinstance(act, (bytes, bytearray)):
+        raise ValueError("activation must be bytes-like")
+    return (_I32.pack(int(msg["expert_id"])) + _I32.pack(int(msg["batch_size"])) +
+            _I32.pack(int(msg["hidden_dim"])) + _U32.pack(int(msg["input_dtype"])) +
+            _U32.pack(int(msg["output_dtype"])) + _U32.pack(len(act)) + bytes(act))
+
+
+def decode_infer_response(body: bytes):
+    off = 0
+    vals = []
+    for what in ("status_code", "batch_size", "hidden_dim"):
+        b, off = _take(body, off, 4, what)
+        vals.append(_I32.unpack(b)[0])
+    b, off = _take(body, off, 4, "output_dtype")
+    out_dt = _U32.unpack(b)[0]
+    b, off = _take(body, off, 4, "output_nbytes")
+    nb = _U32.unpack(b)[0]
+    out, off = _take(body, off, nb, "output")
+    if off != len(body):
+        raise ProtocolError(f"infer_response has trailing bytes: parsed {off}, total {len(body)}")
+    return {"status_code": vals[0], "batch_size": vals[1], "hidden_dim": vals[2],
+            "output_dtype": out_dt, "output": out}
 
 
 def _take(body: bytes, off: int, n: int, what: str):

@@ -56,7 +56,7 @@ CX_API const char* cx_version(void);
  * backend_registry_v2.h:12-19).  The glue maps these fields onto
  * common::StaticGpuInfo / DynamicGpuInfo (common/types.h:85-110). */
 typedef struct cx_device_info {
-    char name[128];          /* marketing name, e.g. "AMD Instinct MI355X"  */
+    char name[128];          /* marketing name, e.g. "AMD Instinct MI355X"; "AMD gfx950" when the host has no name table */
     char arch[64];           /* gcnArchName, e.g. "gfx950:sramecc+:xnack-"  */
     uint64_t total_mem_bytes;
     uint64_t free_mem_bytes;
