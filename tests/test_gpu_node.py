@@ -236,6 +236,39 @@ def test_moe_layer_request_status(node):
         w.close()
 
 
+def test_remote_node_over_socket_equals_local_node(node, gpu):
+    """moe_dispatch.RemoteNode over a real worker socket (the integrated loop)
+    gives the same bf16 partial as a LocalNode on the same experts in this
+    process: the server-side dispatch without a host round trip per expert."""
+    from constellation_amd.engine import Expert, Layer
+    from constellation_amd.moe_dispatch import LocalNode, RemoteNode, run_topk_moe_layer
+    print("[node] RemoteNode over a socket", flush=True)
+    T, K = 4, 3
+    rng = np.random.default_rng(3)
+    ids = np.stack([rng.choice(LOCAL, K, replace=False) for _ in range(T)]).astype(np.int32)
+    wts = rng.uniform(0.1, 1.0, ids.shape).astype(np.float32)
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(torch.bfloat16).cuda()
+    w = node.layer_worker()
+    local = {}
+    try:
+        remote = RemoteNode.over_socket(w.sock, {LAYER: LOCAL}, shared_layers=[LAYER])
+        y_remote = run_topk_moe_layer([remote], x, LAYER, ids, wts)
+        for l in LOCAL + [EPL]:
+            ex = node.experts[SHARED_ID if l == EPL else gid(l)]
+            local[l] = Expert.upload(0, ex["w_up"], ex["s_up"], ex["w_gate"], ex["s_gate"],
+                                     ex["w_down"], ex["s_down"])
+        layer = Layer(gpu, [local.get(i) for i in range(EPL)], local[EPL])
+        y_local = run_topk_moe_layer([LocalNode({LAYER: layer})], x, LAYER, ids, wts)
+        torch.cuda.synchronize()
+        layer.close()
+        assert torch.equal(y_remote.view(torch.int16), y_local.view(torch.int16))
+    finally:
+        w.close()
+        torch.cuda.synchronize()
+        for e in local.values():
+            e.free()
+
+
 def test_upload_while_a_worker_infers(node):
     """resident_bg uploads (UploadExpertAmdV2 on the control side) while the
     worker thread serves requests: every answer stays identical."""
