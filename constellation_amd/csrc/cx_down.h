@@ -153,3 +153,177 @@ __device__ __forceinline__ void down_item_path(const ExpertLaunch& L, const Unit
 inline size_t down_item_lds(int inter) { return (size_t)2 * kDownLdsRows * ((size_t)inter * 2 + 16); }
 
 }  // namespace cx
+
+namespace cx {
+
+// ---------------------------------------------------------------------------
+// One-token decode: down projection of every item and the weighted combine in
+// one launch.  Workgroup = 16 output rows x all items: wave w streams routed
+// item w's 16 rows over the full K (NKB k-blocks), then its share (NKS
+// k-blocks) of the shared expert's K, as one weight ring; the h rows it needs
+// (routed item: all of K; shared expert: its k range) are DMA'd into the
+// wave's own LDS slice first.  The output rows are then combined in LDS —
+// routes in route order weighted by topk_w, the shared expert's k-range
+// partials in wave order, added last — cast, and stored.  Every CU streams
+// from eight experts at once, and neither y_part nor a combine launch is
+// needed.  Semantics: RunDownReferenceV2 (expert_reference_v2.cc:92-144) per
+// expert and combine_outputs_torch (server/moe_layer_runtime.py:148-167),
+// shared expert last (full_model_runtime.py:348).
+// Plan layout at T = 1 (dec_plan_core): routed item i = slot i owns pair
+// s0 + i (s0 = 1 with a shared expert, whose pair is 0), token_pairs[k] =
+// pair of route k or -1.
+constexpr int kDc1Waves = 8;
+
+template <int NKB>
+struct Dc1Geom {
+    static constexpr int NKS = NKB >= kDc1Waves ? NKB / kDc1Waves : 1;  // shared k-blocks per wave
+    static constexpr int kRoutedBytes = NKB * kKB * 2;                   // one h plane of a routed item
+    static constexpr int kSharedBytes = NKS * kKB * 2;                   // one plane of a shared slice
+    static constexpr int kWaveBytes = 2 * kRoutedBytes + 2 * kSharedBytes;
+    static constexpr int kRedOff = kDc1Waves * kWaveBytes;
+    static constexpr int kLds = kRedOff + 2 * kDc1Waves * 4 * 16;      // + routed / shared row partials
+};
+
+// One wave's ring: NR routed stages (item weights pd, scales scd) then NS
+// shared stages (ps, scs); h of stage k read from the wave's LDS slice.
+template <int NR, int NS, int D, int NKB>
+__device__ __forceinline__ void dc1_ring(const uint8_t* pd, const uint8_t* ps, const float* scd,
+                                         const float* scs, const unsigned char* hw, int g,
+                                         f32x4* acc_r, f32x4* acc_s) {
+    typedef Dc1Geom<NKB> G;
+    constexpr int NK = NR + NS;
+    constexpr int DP = D < NK ? D : NK;  // prologue stages
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 ar = zero, as = zero;
+    auto wptr = [&](int k) { return k < NR ? pd + k * kKB : ps + (k - NR) * kKB; };
+    u32x4 wb[D][2];
+#pragma unroll
+    for (int s = 0; s < DP; ++s) {
+        wb[s][0] = ld16(wptr(s));
+        wb[s][1] = ld16(wptr(s) + 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float sc[NK];
+#pragma unroll
+    for (int k = 0; k < NK; ++k) sc[k] = k < NR ? ldsc(scd + k) : ldsc(scs + (k - NR));
+    // the DMA'd h is older than the ring's loads; nothing of the loop may
+    // move above this wait (the compiler cannot count LDS DMA exactly and
+    // would drain the ring with vmcnt(0))
+    vm_wait<2 * DP>();
+    lds_dma_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+        const int s = k % D;
+        const unsigned char* hp = k < NR ? hw + k * (kKB * 2) + g * 64
+                                         : hw + 2 * G::kRoutedBytes + (k - NR) * (kKB * 2) + g * 64;
+        const int lo = k < NR ? G::kRoutedBytes : G::kSharedBytes;
+        u32x4 hb[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            hb[j] = *reinterpret_cast<const u32x4*>(hp + 16 * j);
+            hb[4 + j] = *reinterpret_cast<const u32x4*>(hp + lo + 16 * j);
+        }
+        const f32x4 t = down_step(wb[s], hb);
+        if (k < NR) ar += sc[k] * t;
+        else as += sc[k] * t;
+        __builtin_amdgcn_sched_barrier(0);
+        if (k + D < NK) {
+            wb[s][0] = ld16(wptr(k + D));
+            wb[s][1] = ld16(wptr(k + D) + 16);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    *acc_r = ar;
+    *acc_s = as;
+}
+
+// Row tile `rtile` (16 output rows).  The plan header and the wave's item
+// record come first, then the h DMA and the ring.  Wave 0 fetches the route
+// table with the DMA, so the combine needs no memory round trip.
+template <int NKB, int D>
+__device__ __forceinline__ void down_comb1_tile(const ExpertLaunch& L, const int* token_pairs,
+                                                const float* topk_w, int top_k, unsigned char* lds,
+                                                int rtile) {
+    typedef Dc1Geom<NKB> G;
+    constexpr int NKS = G::NKS;
+    const int I = L.inter;
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int g = lane >> 4, c = lane & 15;
+    const int r0 = rtile * kTileRows;
+    const PlanHdr hd = ld_uniform(L.plan.hdr);
+    const int ts = hd.n_routed_items;
+    const bool shared = hd.n_items > ts;
+    const bool has_r = wave < ts;
+    const bool has_s = shared && wave * NKS < NKB;
+    unsigned char* hw = lds + wave * G::kWaveBytes;
+    const uint8_t* pd = nullptr;
+    const uint8_t* ps = nullptr;
+    const float* scd = nullptr;
+    const float* scs = nullptr;
+    // 0) h into this wave's LDS slice (1 KB per wave instruction), before any weight load
+    if (has_r) {
+        const ItemRec ri = ld_uniform(L.plan.item_rec + wave);
+        const uint16_t* hh = L.h_hi + (size_t)ri.pb * I + lane * 8;
+        const uint16_t* hl = L.h_lo + (size_t)ri.pb * I + lane * 8;
+#pragma unroll
+        for (int j = 0; j < G::kRoutedBytes / 1024; ++j) {
+            __builtin_amdgcn_global_load_lds(hh + j * 512, hw + j * 1024, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(hl + j * 512, hw + G::kRoutedBytes + j * 1024, 16, 0, 0);
+        }
+        pd = ri.w_down + (size_t)(r0 + c) * I + g * 32;
+        scd = ri.s_down + (size_t)__builtin_amdgcn_readfirstlane(r0 / ri.down_rb) * (I / kKB);
+    }
+    if (has_s) {
+        const ItemRec rs = ld_uniform(L.plan.item_rec + ts);
+        constexpr int LPP = G::kSharedBytes / 16;  // lanes per plane
+        const size_t k0 = (size_t)wave * NKS * kKB;
+        if (lane < 2 * LPP) {
+            const uint16_t* src = (lane < LPP ? L.h_hi : L.h_lo) + (size_t)rs.pb * I + k0 + (lane % LPP) * 8;
+            __builtin_amdgcn_global_load_lds(src, hw + 2 * G::kRoutedBytes, 16, 0, 0);
+        }
+        ps = rs.w_down + (size_t)(r0 + c) * I + k0 + g * 32;
+        scs = rs.s_down + (size_t)__builtin_amdgcn_readfirstlane(r0 / rs.down_rb) * (I / kKB) + wave * NKS;
+    }
+    // wave 0: the route table (lane k: pair and weight of route k), issued
+    // with the DMA so that the ring's first wait covers it
+    int tpl = -1;
+    float twl = 0.f;
+    if (wave == 0 && lane <= top_k) {
+        tpl = token_pairs[lane];
+        if (lane < top_k) twl = topk_w[lane];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 ar, as;
+    if (has_r && has_s) dc1_ring<NKB, NKS, D, NKB>(pd, ps, scd, scs, hw, g, &ar, &as);
+    else if (has_r) dc1_ring<NKB, 0, D, NKB>(pd, ps, scd, scs, hw, g, &ar, &as);
+    else if (has_s) dc1_ring<0, NKS, D, NKB>(pd, ps, scd, scs, hw, g, &ar, &as);
+    else {
+        lds_dma_barrier();
+        ar = as = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    // 1) column 0 (the token) of each wave's tiles: rows 4g..4g+3 on lane 16g
+    f32x4* red_r = reinterpret_cast<f32x4*>(lds + G::kRedOff);
+    f32x4* red_s = red_r + kDc1Waves * 4;
+    if (c == 0) {
+        red_r[wave * 4 + g] = ar;
+        red_s[wave * 4 + g] = as;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const int s0 = shared ? 1 : 0;
+        f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < top_k; ++k) {
+            const int p = __shfl(tpl, k);
+            const float wk = __shfl(twl, k);
+            if (p >= s0) sum += wk * red_r[(p - s0) * 4 + (lane & 3)];
+        }
+        if (shared && __shfl(tpl, top_k) >= 0) {
+#pragma unroll
+            for (int w = 0; w < kDc1Waves; ++w) sum += red_s[w * 4 + (lane & 3)];
+        }
+        if (lane < 4) store_out4(L.y, L.y_f32, (size_t)r0 + 4 * lane, sum, L.out_dtype);
+    }
+}
+
+}  // namespace cx

@@ -458,6 +458,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 }
 
 // ---------------------------------------------------------------------------
+// One-token decode: down projection of every item plus the weighted combine
+// (down_comb1_tile, cx_down.h), grid = hidden/16 workgroups of 8 waves.
+template <int NKB, int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_down_comb1(
+    ExpertLaunch L, const int* __restrict__ token_pairs, const float* __restrict__ topk_w, int top_k) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char dc_lds[];
+    down_comb1_tile<NKB, D>(L, token_pairs, topk_w, top_k, dc_lds, blockIdx.x);
+}
+
+// ---------------------------------------------------------------------------
 // One expert at 1..4 tokens (single mode), as two launches in which every
 // wave's weights are one round trip of loads.  At this size the launches are
 // bound by per-wave latency and MFMA work, not by HBM: the 16-row x full-K
@@ -946,6 +956,39 @@ hipError_t launch_down_ks(const ExpertLaunch& L, hipStream_t s) {
     const dim3 grid(L.hidden / (kDownKsGroups * kTileRows)), block(512);
     if (L.inter / kKB == 16) cx_launch((k_down_ks<4>), grid, block, down_ks_lds(4), s, L);
     else cx_launch((k_down_ks<1>), grid, block, down_ks_lds(1), s, L);
+    return hipGetLastError();
+}
+
+// Ring depth of the one-token down + combine: 8 k-blocks (16 KB) in flight
+// per wave within 128 registers (two 8-wave workgroups per CU).
+constexpr int kDc1Depth = 8;
+
+size_t down_comb1_lds(int inter) {
+    switch (inter / kKB) {
+        case 16: return Dc1Geom<16>::kLds;
+        case 8: return Dc1Geom<8>::kLds;
+        case 4: return Dc1Geom<4>::kLds;
+        default: return 0;
+    }
+}
+
+bool down_comb1_ok(int hidden, int inter, int top_k, int max_lds) {
+    const size_t lds = inter % kKB == 0 ? down_comb1_lds(inter) : 0;
+    return lds > 0 && hidden % kTileRows == 0 && top_k >= 0 && top_k <= kDc1Waves &&
+           (size_t)max_lds >= lds;
+}
+
+hipError_t launch_down_comb1(const ExpertLaunch& L, const int* token_pairs, const float* topk_w,
+                             int top_k, hipStream_t s) {
+    if (L.table == nullptr || L.n_tokens != 1 || !down_comb1_ok(L.hidden, L.inter, top_k, L.max_lds))
+        return hipErrorInvalidValue;
+    const dim3 grid(L.hidden / kTileRows), block(64 * kDc1Waves);
+    const size_t lds = down_comb1_lds(L.inter);
+    switch (L.inter / kKB) {
+        case 16: cx_launch((k_down_comb1<16, kDc1Depth>), grid, block, lds, s, L, token_pairs, topk_w, top_k); break;
+        case 8: cx_launch((k_down_comb1<8, kDc1Depth>), grid, block, lds, s, L, token_pairs, topk_w, top_k); break;
+        default: cx_launch((k_down_comb1<4, 4>), grid, block, lds, s, L, token_pairs, topk_w, top_k); break;
+    }
     return hipGetLastError();
 }
 

@@ -159,6 +159,14 @@ hipError_t launch_combine(const PlanPtrs& plan, const float* y_part, int n_token
 hipError_t launch_combine_dec(const PlanPtrs& plan, const float* topk_w, const float* y_part,
                               int n_tokens, int top_k, int has_shared, int hidden, void* y,
                               int out_dtype, float* y_f32, hipStream_t s);
+// One-token decode (n_tokens == 1, decode plan): down of every item and the
+// weighted combine in one launch, writing y / y_f32 directly (no y_part).
+// Needs top_k <= 8, hidden % 16 == 0, inter / 128 in {4, 8, 16} and
+// down_comb1_lds(inter) bytes of LDS (L.max_lds).
+size_t down_comb1_lds(int inter);
+bool down_comb1_ok(int hidden, int inter, int top_k, int max_lds);
+hipError_t launch_down_comb1(const ExpertLaunch& L, const int* token_pairs, const float* topk_w,
+                             int top_k, hipStream_t s);
 hipError_t launch_plan(const int32_t* ids, const float* w, int n_tokens, int top_k,
                        const cx_expert_desc* table, int n_experts, int has_shared,
                        int item_cap, int max_items, PlanPtrs plan, int* err_flag,

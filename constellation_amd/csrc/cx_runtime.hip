@@ -605,13 +605,21 @@ int moe_decode(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, 
     // down: the routed items and the shared expert's item (last)
     L.skip_shared = 0;
     L.max_items = routed_items + layer->has_shared;
+    L.max_lds = ctx->max_lds;
+    const float* route_w = route != nullptr ? route->wout : w;
+    if (T == 1 && down_comb1_ok(layer->hidden, layer->inter, top_k, ctx->max_lds)) {
+        // one token: down of every item and the combine in one launch
+        Span sp(ctx, "down", s);
+        CX_HIP(launch_down_comb1(L, P.token_pairs, route_w, top_k, s));
+        return CX_OK;
+    }
     if (L.max_items > 0) {
         Span sp(ctx, "down", s);
         CX_HIP(launch_down(L, s));
     }
     {
         Span sp(ctx, "combine", s);
-        CX_HIP(launch_combine_dec(P, route != nullptr ? route->wout : w, L.y_part, T, top_k,
+        CX_HIP(launch_combine_dec(P, route_w, L.y_part, T, top_k,
                                   layer->has_shared, layer->hidden, y, out_dtype, y_f32, s));
     }
     return CX_OK;

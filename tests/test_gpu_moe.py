@@ -270,7 +270,7 @@ def test_full_size_decode_layer(gpu, oracle, T):
         _free(layer, experts, sh)
 
 
-@pytest.mark.parametrize("T,prefill", [(2, False), (20, True)])
+@pytest.mark.parametrize("T,prefill", [(1, False), (2, False), (20, True)])
 def test_moe_duplicate_route_is_dropped_and_reported(gpu, oracle, T, prefill):
     """validate_routes (server/moe_layer_runtime.py:84-98) rejects a token that
     lists the same expert twice; the engine drops the repeat and reports it."""
@@ -291,6 +291,38 @@ def test_moe_duplicate_route_is_dropped_and_reported(gpu, oracle, T, prefill):
         kept[0] = [2, -1]
         ref = _oracle_moe(oracle, cpu, None, x.float().cpu().numpy(), kept, wts)
         assert rel_l2(yf.cpu().numpy(), ref) < 1e-5
+    finally:
+        _free(layer, experts, sh)
+
+
+@pytest.mark.parametrize("H,I,shared,K,dtype,odtype", [
+    (1024, 512, True, 8, torch.bfloat16, torch.bfloat16),
+    (1024, 1024, False, 4, torch.float16, torch.float16),
+    (2048, 2048, True, 6, torch.bfloat16, torch.float16),
+    (1024, 512, True, 1, torch.float16, torch.bfloat16),
+    (1024, 2048, False, 8, torch.bfloat16, torch.bfloat16)])
+def test_one_token_down_combine(gpu, oracle, H, I, shared, K, dtype, odtype):
+    """One token (cx_moe_decode, routes given): the down projection of every
+    item and the weighted combine run as one launch (k_down_comb1) for top_k
+    <= 8 — inter of 4, 8 and 16 k-blocks, with and without a shared expert,
+    fewer routes than waves, mixed in/out dtypes."""
+    print(f"[moe] one-token down+combine H={H} I={I} shared={shared} K={K}", flush=True)
+    E = 16
+    layer, experts, sh, cpu, cpu_sh = _make_layer(gpu, oracle, E, H, I, seed=81 + K, shared=shared)
+    try:
+        x = gpu.gen_normal(82 + K, 1, (1, H), 1.0, dtype)
+        rng = np.random.default_rng(K)
+        ids = rng.choice(E, size=(1, K), replace=False).astype(np.int32)
+        wts = rng.uniform(0.1, 1.0, size=(1, K)).astype(np.float32)
+        y, yf = gpu.moe(layer, x, torch.from_numpy(ids).cuda(), torch.from_numpy(wts).cuda(),
+                        out_dtype=odtype, want_f32=True)
+        gpu.sync()
+        ref = _oracle_moe(oracle, cpu, cpu_sh, x.float().cpu().numpy(), ids, wts)
+        yf = yf.cpu().numpy()
+        assert rel_l2(yf, ref) < 1e-5, rel_l2(yf, ref)
+        assert np.abs(yf - ref).max() < 2e-2
+        code = BF16 if odtype == torch.bfloat16 else FP16
+        assert np.array_equal(_bits(y), oracle.encode_act(yf, code, "rne"))
     finally:
         _free(layer, experts, sh)
 
