@@ -49,7 +49,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--pool", type=int, default=64, help="distinct tokens rotated per step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-b16", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU baseline time budget")
     ap.add_argument("--no-extra-configs", action="store_true",
                     help="skip the single-expert, prefill and node-share measurements")
     ap.add_argument("--extras", default="h,0,3,4",
@@ -363,17 +363,43 @@ def bench_node_share(ctx, sweeps):
     return out
 
 
+def host_cpu_info() -> dict:
+    """CPU model, socket count and the CPUs this process may use."""
+    model, sockets = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k = k.strip()
+                if k == "model name" and model == "unknown":
+                    model = v.strip()
+                elif k == "physical id":
+                    sockets.add(v.strip())
+    except OSError:
+        pass
+    try:
+        visible = len(os.sched_getaffinity(0))
+    except AttributeError:
+        visible = os.cpu_count() or 1
+    return {"model": model, "sockets": max(1, len(sockets)), "cpus_visible": visible}
+
+
 def cpu_baseline(budget_s: float):
     """Reference CPU expert path on host cores: per token, the fp64 router
     (this repo's port) + 9 sequential expert runs through the reference's own
-    RunFusedUpGateCpuV2/RunDownCpuV2 (oracle/_ref) with 12 OpenMP threads."""
+    RunFusedUpGateCpuV2/RunDownCpuV2 (oracle/_ref), batch 1 per run as the
+    reference's CPU worker serves it.  Timed with the 12 OpenMP threads the
+    reference hard-codes (backend_cpu_v2.cc:245-246) and with every visible
+    host CPU; a cold-cache expert time after a 256 MB flush as the reference's
+    CPU benchmark does (cpu_benchmark_support_v2.cc:203-219); configs 0, 2, 3
+    and 4 derived from those per-run times (stated in `per_config`)."""
     import numpy as np
     root = os.path.dirname(os.path.abspath(__file__))
     sys.path.insert(0, root)
     from oracle.oracle import BF16, Oracle, RefCpu
     o = Oracle()
     kind = "reference" if RefCpu.available() else "port"
-    threads = 12
+    host = host_cpu_info()
     n_pool = 12  # 12 x 44 MB experts, far beyond the host LLC
     experts = [o.gen_expert(SEED, stream_base(0, e)) for e in range(n_pool)]
     shared = o.gen_expert(SEED, stream_base(0, E))
@@ -384,29 +410,79 @@ def cpu_baseline(budget_s: float):
     if kind == "reference":
         ref = RefCpu()
         runners = [ref.cpu_expert(ex) for ex in experts + [shared]]
-        run = lambda r, x: r.run(x, BF16, BF16, threads)  # noqa: E731
+        run = lambda r, x, th: r.run(x, BF16, BF16, th)  # noqa: E731
     else:
         runners = experts + [shared]
-        run = lambda ex, x: o.expert_cpu_baseline(ex, x, BF16, BF16, threads)  # noqa: E731
-    run(runners[0], xs[0])  # warm
-    t0 = time.perf_counter()
-    tokens = 0
-    while True:
-        x = xs[tokens % 64]
-        o.route(o.decode_act(x, BF16), w_r, bias)
-        for j in range(TOPK):
-            run(runners[(tokens * TOPK + j) % n_pool], x)
-        run(runners[-1], x)
-        tokens += 1
-        if time.perf_counter() - t0 > budget_s:
-            break
-    dt = time.perf_counter() - t0
+        run = lambda ex, x, th: o.expert_cpu_baseline(ex, x, BF16, BF16, th)  # noqa: E731
+    run(runners[0], xs[0], 12)  # warm
+
+    def per_token(threads: int, secs: float):
+        t0 = time.perf_counter()
+        tokens = 0
+        while True:
+            x = xs[tokens % 64]
+            o.route(o.decode_act(x, BF16), w_r, bias)
+            for j in range(TOPK):
+                run(runners[(tokens * TOPK + j) % n_pool], x, threads)
+            run(runners[-1], x, threads)
+            tokens += 1
+            if time.perf_counter() - t0 > secs:
+                break
+        return (time.perf_counter() - t0) / tokens * 1e6, tokens
+
+    def per_expert(threads: int, secs: float):
+        t0 = time.perf_counter()
+        n = 0
+        while True:
+            run(runners[n % n_pool], xs[n % 64], threads)
+            n += 1
+            if time.perf_counter() - t0 > secs:
+                break
+        return (time.perf_counter() - t0) / n * 1e6, n
+
+    flush_buf = np.zeros(256 * 1024 * 1024 // 8, np.uint64)
+
+    def cold_expert(threads: int, n: int):
+        ts = []
+        for i in range(n):
+            np.add(flush_buf, 1, out=flush_buf)  # evict the caches (256 MB written)
+            t0 = time.perf_counter()
+            run(runners[i % n_pool], xs[i % 64], threads)
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts)) * 1e6
+
+    all_cores = host["cpus_visible"]
+    tok12, ntok12 = per_token(12, budget_s * 0.5)
+    tok_all, ntok_all = per_token(all_cores, budget_s * 0.25)
+    exp12, nexp12 = per_expert(12, budget_s * 0.15)
+    cold12 = cold_expert(12, 10)
+    router_us = max(tok12 - 9 * exp12, 0.0)
     for r in runners:
         if hasattr(r, "close"):
             r.close()
-    return {"value": dt / tokens * 1e6, "unit": "us/token", "cores": threads, "kind": kind,
-            "sample": f"{tokens} tokens x (fp64 router port + 9 sequential expert runs), "
-                      f"12 resident experts rotated, bf16 in/out, {os.cpu_count()} host CPUs visible"}
+    per_config = {
+        "config0_us_per_expert": exp12,
+        "config0_sample": f"{nexp12} single-token expert runs, 12 experts rotated, 12 threads",
+        "config1_us_per_token": tok12,
+        "config1_us_per_token_all_cores": tok_all,
+        "all_cores_threads": all_cores,
+        "config1_all_cores_sample": f"{ntok_all} tokens x (router + 9 runs), {all_cores} threads",
+        "expert_cold_us": cold12,
+        "expert_cold_sample": "median of 10 runs, each after a 256 MB write flush, 12 threads",
+        "config2_us_per_layer": 16 * tok12,
+        "config3_ms_per_chunk": 512 * tok12 / 1e3,
+        "config4_ms_per_sweep": 58 * 32 * TOPK * cold12 / 1e3,
+        "derivation": "configs 2 and 3 = 16 and 512 x the measured per-token time (router + 9 "
+                      "sequential batch-1 runs, as the reference's single CPU worker serves "
+                      "them); config 4 = 58 layers x 32 tokens x 8 routed runs x the cold "
+                      "per-expert time (extrapolated, not run)",
+    }
+    return {"value": tok12, "unit": "us/token", "cores": 12, "kind": kind,
+            "sample": f"{ntok12} tokens x (fp64 router port + 9 sequential expert runs), "
+                      f"12 resident experts rotated, bf16 in/out, 12 OpenMP threads; host "
+                      f"{host['model']}, {host['sockets']} socket(s), {host['cpus_visible']} "
+                      f"CPUs visible to this process",
+            "host": host, "router_us_per_token": router_us, "per_config": per_config}
 
 
 def main() -> int:
