@@ -601,16 +601,17 @@ __global__ __launch_bounds__(512) void k_down_ks(ExpertLaunch L) {
 
 // ---------------------------------------------------------------------------
 // Grouped GEMM for items of up to 64 pairs (cx_grouped.h): gate/up over
-// inter/64 row tiles x items as a one-dimensional XCD-aware grid
-// (xcd_tile_item: an item's x rows stay in one L2), down over grid =
-// (hidden/256, items) (measured: the XCD mapping does not help it).  LDS rings
-// of 80 KB / 128 KB: two gate/up or one down workgroup per CU.
+// grid = inter/128 row tiles x items (one dimension, an item's tiles
+// consecutive, so they spread over the XCDs), down over grid = (hidden/256,
+// items).  Measured at config 3: the XCD-aware placement (all tiles of an item
+// on one XCD, its x rows in one L2) streamed 2.5 % slower for the gate/up and
+// 5 % slower for the down than the spread placement.  Both kernels are 8-wave
+// workgroups at two waves per SIMD: one per CU.
 template <int NKB, bool F16, bool SINGLE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_gu_grp(ExpertLaunch L) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k_gu_grp(ExpertLaunch L) {
     extern __shared__ __attribute__((aligned(16))) unsigned char grp_lds[];
-    int tile, item;
-    xcd_tile_item(blockIdx.x, L.inter / kGuGrpRows, &tile, &item);
-    grp_gate_up_tile<NKB, F16, SINGLE>(L, tile, item, grp_lds);
+    const int n_tiles = L.inter / kGuGrpRows;
+    grp_gate_up_tile<NKB, F16, SINGLE>(L, blockIdx.x % n_tiles, blockIdx.x / n_tiles, grp_lds);
 }
 
 template <int NKB, bool SINGLE>
@@ -839,12 +840,13 @@ bool grp_ok(const ExpertLaunch& L) {
 
 template <int NKB, bool F16>
 void go_gu_grp(const ExpertLaunch& L, dim3 grid, hipStream_t s) {
-    if (L.table == nullptr) cx_launch((k_gu_grp<NKB, F16, true>), grid, dim3(256), grp_gu_lds(), s, L);
-    else cx_launch((k_gu_grp<NKB, F16, false>), grid, dim3(256), grp_gu_lds(), s, L);
+    const dim3 block(64 * kGuGrpWaves);
+    if (L.table == nullptr) cx_launch((k_gu_grp<NKB, F16, true>), grid, block, grp_gu_lds(), s, L);
+    else cx_launch((k_gu_grp<NKB, F16, false>), grid, block, grp_gu_lds(), s, L);
 }
 
 bool pick_gu_grp(const ExpertLaunch& L, int items, hipStream_t s) {
-    const dim3 grid(xcd_grid(L.inter / kGuGrpRows, items));
+    const dim3 grid((L.inter / kGuGrpRows) * items);
     const bool f16 = L.in_dtype == CX_DTYPE_FP16;
     switch (L.hidden / kKB) {
         case 56: f16 ? go_gu_grp<56, true>(L, grid, s) : go_gu_grp<56, false>(L, grid, s); return true;

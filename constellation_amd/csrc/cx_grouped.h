@@ -7,8 +7,9 @@
 //
 // Why this shape.  The activations of an item (x rows for gate/up, h rows for
 // down) are shared by every weight row of the tile, so they go through LDS.
-// For each 128-column k-block, the workgroup's waves each load one quarter
-// (one "piece") of the item's activation block into registers.  They issue
+// For each 128-column k-block, the workgroup's waves each load a share of
+// the item's activation block into registers (gate/up: half a 1 KB "piece"
+// per wave; down: one piece per wave and h plane).  They issue
 // it together with that k-block's weights, D k-blocks ahead, in the same
 // register ring.  Just before the k-block is used, the pieces are written
 // to one of two LDS slots and a barrier publishes them.  Every vector load
@@ -29,9 +30,12 @@ constexpr int kGrpPairs = kTileTok * kGrpTiles;      // 64 pairs per item
 constexpr size_t kPiece = 1024;                      // one wave load (64 x 16 B)
 constexpr size_t kActBlk = 4 * kPiece;               // 16 pairs x 128 k x 16 bit
 
-// gate/up: 4 waves x 16 rows of gate and of up, D-deep register ring; two
-// LDS slots of kGrpTiles activation blocks.
-constexpr int kGuGrpRows = kTileRows * kWaves;  // 64
+// gate/up: 8 waves x 16 rows of gate and of up, D-deep register ring; two
+// LDS slots of kGrpTiles activation blocks.  Each wave loads half a piece
+// (8 B per lane) of every column tile per k-block, so one activation block
+// serves 128 weight rows.
+constexpr int kGuGrpWaves = 8;
+constexpr int kGuGrpRows = kTileRows * kGuGrpWaves;  // 128
 constexpr int kGuGrpD = 4;
 constexpr size_t grp_gu_lds() { return (size_t)2 * kGrpTiles * kActBlk; }  // 32 KB
 
@@ -51,21 +55,9 @@ __device__ __forceinline__ void lds_write_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// XCD-aware placement of a (row tile, item) grid launched as one dimension
-// of n_tiles * round_up(items, 8) workgroups.  Workgroups are dealt to the 8
-// XCDs round-robin, so linear id w runs on XCD w % 8.  Every row tile of one
-// item is mapped to the same XCD (item = 8 * (j / n_tiles) + w % 8,
-// tile = j % n_tiles with j = w / 8), so the item's activation rows are
-// fetched into that XCD's L2 only, and reused there by all its tiles.
-constexpr int kXcds = 8;
-
-__device__ __forceinline__ void xcd_tile_item(int w, int n_tiles, int* tile, int* item) {
-    const int j = w / kXcds;
-    *tile = j % n_tiles;
-    *item = (j / n_tiles) * kXcds + (w % kXcds);
-}
-
-inline int xcd_grid(int n_tiles, int items) { return n_tiles * ((items + kXcds - 1) / kXcds) * kXcds; }
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(1))) const u32x2 global_u32x2;
+__device__ __forceinline__ u32x2 ld8(const void* p) { return *(global_u32x2*)(p); }
 
 // Scale of k-block k of the lane-distributed scale row `v` (lane l holds
 // k-block l).
@@ -173,17 +165,19 @@ __device__ __forceinline__ void grp_gate_up_item(const ExpertLaunch& L, const Un
     const int rbu = __builtin_amdgcn_readfirstlane(r0 / u.e.up_rb);
     float scg_v = lane < NKB ? ldf(u.e.s_gate + (size_t)rbg * NKB + lane) : 0.f;
     float scu_v = lane < NKB ? ldf(u.e.s_up + (size_t)rbu * NKB + lane) : 0.f;
-    // activation pieces: this wave loads piece j = wave of every column tile;
-    // lane (c, g) carries pair tt*16 + c, elements 8*(4g + wave) .. +7.
+    // activation pieces: wave w loads half h = w % 2 of piece j = w / 2 of
+    // every column tile; lane (c, g) carries pair tt*16 + c, elements
+    // 8*(4g + j) + 4h .. +3.
+    const int pj = wave >> 1, ph = wave & 1;
     const uint16_t* xs[NT];
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) {
         const int q = min(tt * kTileTok + c, u.np - 1);
         const int tok = SINGLE ? u.pb + q : ldi(L.plan.pair_token + u.pb + q);
-        xs[tt] = static_cast<const uint16_t*>(L.x) + (size_t)tok * H + 8 * (4 * g + wave);
+        xs[tt] = static_cast<const uint16_t*>(L.x) + (size_t)tok * H + 8 * (4 * g + pj) + 4 * ph;
     }
     u32x4 wb[D][4];
-    u32x4 xr[D][NT];
+    u32x2 xr[D][NT];
     f32x4 accg[NT], accu[NT];
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) {
@@ -196,12 +190,12 @@ __device__ __forceinline__ void grp_gate_up_item(const ExpertLaunch& L, const Un
         wb[s][2] = ld16(pu + (size_t)k * kKB);
         wb[s][3] = ld16(pu + (size_t)k * kKB + 16);
 #pragma unroll
-        for (int tt = 0; tt < NT; ++tt) xr[s][tt] = ld16(xs[tt] + (size_t)k * kKB);
+        for (int tt = 0; tt < NT; ++tt) xr[s][tt] = ld8(xs[tt] + (size_t)k * kKB);
     };
     auto publish = [&](int s, int slot) {
-        unsigned char* dst = lds + (size_t)slot * SLOT + wave * kPiece + lane * 16;
+        unsigned char* dst = lds + (size_t)slot * SLOT + pj * kPiece + lane * 16 + 8 * ph;
 #pragma unroll
-        for (int tt = 0; tt < NT; ++tt) *reinterpret_cast<u32x4*>(dst + tt * kActBlk) = xr[s][tt];
+        for (int tt = 0; tt < NT; ++tt) *reinterpret_cast<u32x2*>(dst + tt * kActBlk) = xr[s][tt];
     };
     auto compute = [&](int k, int s, int slot) {
         const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
