@@ -52,10 +52,11 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU baseline time budget")
     ap.add_argument("--no-extra-configs", action="store_true",
                     help="skip the single-expert, prefill and node-share measurements")
-    ap.add_argument("--extras", default="h,0,3,4",
+    ap.add_argument("--extras", default="h,0,3,c,4",
                     help="comma list of the extra measurements: h host boundary at B=1 "
                          "(layer request vs per-expert requests), 0 single expert, "
-                         "3 prefill chunk, 4 node share (default: all)")
+                         "3 prefill chunk, c compute-bound prefill shape (not a BASELINE "
+                         "config), 4 node share (default: all)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="first run a plain device copy of this many MiB (three times): the "
                          "known-size kernel that scales HBM counters of a --pmc profile")
@@ -308,6 +309,46 @@ def bench_prefill(ctx, layers, steps):
                         for k, (n, t) in kern.items()}}
 
 
+def bench_compute_bound(ctx, layers, steps):
+    """Supplementary prefill shape, not a BASELINE config: 4096 tokens, each
+    routed to 8 of 64 experts (token t -> experts (8t + k) mod 64, weight 1/8),
+    so every routed expert sees 512 tokens, plus the shared expert on all 4096.
+    At 2n FLOP per weight byte this is past the bf16 MFMA ridge (~312 FLOP/B),
+    so it reports the grouped GEMM's rate against the 2.5 PFLOP/s bf16 peak."""
+    import torch
+    T, n_exp = 4096, 64
+    x = ctx.gen_normal(SEED, 0x7100, (T, H), 1.0, torch.bfloat16)
+    t = torch.arange(T, dtype=torch.int32).unsqueeze(1)
+    k = torch.arange(TOPK, dtype=torch.int32).unsqueeze(0)
+    ids = ((t * TOPK + k) % n_exp).to(torch.int32).cuda()
+    w = torch.full((T, TOPK), 1.0 / TOPK, dtype=torch.float32, device="cuda")
+    lay = layers[0]["layer"]
+    ctx.moe(lay, x, ids, w, prefill=True)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        ctx.moe(lay, x, ids, w, prefill=True)
+    ev1.record()
+    torch.cuda.synchronize()
+    ctx.sync()
+    ms = ev0.elapsed_time(ev1) / steps
+    ctx.profile(True)
+    ctx.moe(lay, x, ids, w, prefill=True)
+    torch.cuda.synchronize()
+    kern = {k: ctx.profile_read(k) for k in ("plan", "gate_up", "down", "combine")}
+    ctx.profile(False)
+    pairs = T * TOPK + T
+    flops = pairs * 6.0 * I * H
+    tfl = flops / (ms * 1e-3) / 1e12
+    return {"label": "supplementary compute-bound shape, not a BASELINE config",
+            "tokens": T, "routed_experts": n_exp, "tokens_per_routed_expert": T * TOPK // n_exp,
+            "pairs": pairs, "ms_per_chunk": ms, "flop": flops, "tflops": tfl,
+            "frac_of_bf16_peak": tfl / 2500.0, "frac_of_fp8_peak": tfl / 5000.0,
+            "kernels": {k: {"launches": n, "avg_us": (t * 1e3 / n) if n else None}
+                        for k, (n, t) in kern.items()}}
+
+
 def bench_node_share(ctx, sweeps):
     """Config 4: one expert node's resident share, 58 layers x 64 experts
     (e = 0 mod 4, no shared expert; ~163.5 GB), batch 32 per layer with routes
@@ -530,6 +571,8 @@ def main() -> int:
         extras["config0_single_expert"] = bench_single_expert(ctx, layers, max(100, args.steps // 2))
     if "3" in want:
         extras["config3_prefill"] = bench_prefill(ctx, layers, 10)
+    if "c" in want:
+        extras["prefill_compute_bound"] = bench_compute_bound(ctx, layers, 5)
     for L in layers:  # release the rotated layers before the node-share residency
         L["layer"].close()
         for e in L["experts"] + [L["shared"]]:
