@@ -60,10 +60,31 @@ def _compile(name: str, extra: list[str]) -> Path:
     return obj
 
 
+KBENCH_SRC = PKG / "kbench" / "kbench.hip"
+KBENCH = PKG / "kbench" / "cx_kbench"
+
+
+def build_kbench(verbose: bool = False) -> Path:
+    """The kernel micro-benchmark (constellation_amd/kbench): a stand-alone
+    program that compiles the library's kernels and times single launches."""
+    tmp = KBENCH.with_suffix(".tmp")
+    cmd = [HIPCC, *COMMON, "-o", str(tmp), str(KBENCH_SRC)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("hipcc failed for kbench.hip")
+    os.replace(tmp, KBENCH)
+    if verbose:
+        print(f"built {KBENCH}")
+    return KBENCH
+
+
 def build(verbose: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(4, os.cpu_count() or 1)) as ex:
+    with ThreadPoolExecutor(max_workers=min(5, os.cpu_count() or 1)) as ex:
+        kb = ex.submit(build_kbench, verbose)
         objs = list(ex.map(lambda kv: _compile(*kv), SOURCES.items()))
+        kb.result()
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -1,0 +1,550 @@
+// cx_kbench — kernel-level measurements behind the design notes.  It compiles
+// the library's kernels (cx_expert.hip) into a stand-alone program and times
+// single launches with HIP events on synthetic experts placed as the HBM arena
+// places them (back to back in 2 GiB chunks), so every figure it prints can be
+// reproduced on one MI355X:
+//
+//   cx_kbench layout       grouped gate/up bytes of a config-3-like plan streamed
+//                          bare (no compute) in the natural row-major order and in
+//                          the tiled order a re-layout at upload would give
+//   cx_kbench decode-down  one-token down projection: k_down_comb1 (down + combine
+//                          in one launch) against k_down_item + k_combine_dec
+//   cx_kbench placement    one-token gate/up and down launches with the experts
+//                          packed into one buffer vs spread over 24 x 2 GiB chunks
+//   cx_kbench grouped      the grouped prefill kernels on the config-3-like plan
+//
+// Bytes are synthetic (small finite fp8 codes, block scales 1e-3): the numbers
+// are timings, not results.  Built by constellation_amd/build.py.
+#include "cx_expert.hip"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <random>
+#include <vector>
+
+namespace cx {
+LaunchTimer*& current_launch_timer() {
+    static thread_local LaunchTimer* t = nullptr;
+    return t;
+}
+}  // namespace cx
+
+using namespace cx;
+
+namespace {
+
+#define KB_CHECK(x)                                                                      \
+    do {                                                                                 \
+        hipError_t e_ = (x);                                                             \
+        if (e_ != hipSuccess) {                                                          \
+            std::fprintf(stderr, "HIP error %s at %s:%d\n", hipGetErrorString(e_), __FILE__, \
+                         __LINE__);                                                      \
+            std::exit(1);                                                                \
+        }                                                                                \
+    } while (0)
+
+constexpr int kH = 7168, kI = 2048;
+constexpr size_t kMat = (size_t)kH * kI;
+constexpr size_t kScaleBytes = 16 * 56 * 4;
+constexpr size_t kExpert = 3 * kMat + 3 * kScaleBytes + 1024;  // as laid out in the arena
+constexpr size_t kChunk = 2ull << 30;
+
+__global__ void k_fill_bytes(uint32_t* p, size_t n, uint32_t salt) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        uint64_t z = (i + salt + 0x9E3779B97F4A7C15ull) * 0xBF58476D1CE4E5B9ull;
+        z ^= z >> 31;
+        z *= 0x94D049BB133111EBull;
+        z ^= z >> 29;
+        p[i] = (uint32_t)z & 0x3E3E3E3Eu;  // four finite fp8 codes of magnitude < 1
+    }
+}
+
+__global__ void k_fill_f32(float* p, size_t n, float v) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = v;
+}
+
+// Synthetic experts: `spread` places them back to back in 24 chunks of 2 GiB
+// (1152 experts, ~50 GB, as four resident layer copies occupy the arena);
+// otherwise 48 experts in one 2.1 GB buffer.
+struct Pool {
+    std::vector<uint8_t*> chunks;
+    std::vector<cx_expert_desc> d;
+    explicit Pool(bool spread) {
+        const int per_chunk = (int)(kChunk / kExpert);
+        const int n_chunks = spread ? 24 : 1;
+        const size_t bytes = spread ? kChunk : kExpert * 48;
+        for (int c = 0; c < n_chunks; ++c) {
+            uint8_t* p = nullptr;
+            KB_CHECK(hipMalloc(&p, bytes));
+            k_fill_bytes<<<4096, 256>>>((uint32_t*)p, bytes / 4, 1 + c);
+            chunks.push_back(p);
+        }
+        const int n = spread ? n_chunks * per_chunk : 48;
+        d.resize(n);
+        for (int e = 0; e < n; ++e) {
+            uint8_t* b = spread ? chunks[e / per_chunk] + (size_t)(e % per_chunk) * kExpert
+                                : chunks[0] + (size_t)e * kExpert;
+            cx_expert_desc& q = d[e];
+            q.w_up = b;
+            q.w_gate = b + kMat;
+            q.w_down = b + 2 * kMat;
+            float* s = (float*)(b + 3 * kMat);
+            q.s_up = s;
+            q.s_gate = s + 16 * 56;
+            q.s_down = s + 2 * 16 * 56;
+            k_fill_f32<<<16, 256>>>(s, 3 * 16 * 56, 1e-3f);
+            q.hidden = kH;
+            q.inter = kI;
+            q.up_rb = q.up_cb = q.gate_rb = q.gate_cb = q.down_rb = q.down_cb = 128;
+        }
+        KB_CHECK(hipDeviceSynchronize());
+    }
+    ~Pool() {
+        for (uint8_t* p : chunks) (void)hipFree(p);
+    }
+};
+
+template <class T>
+T* dev_copy(const std::vector<T>& v) {
+    T* p = nullptr;
+    KB_CHECK(hipMalloc(&p, std::max<size_t>(1, v.size()) * sizeof(T)));
+    if (!v.empty()) KB_CHECK(hipMemcpy(p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice));
+    return p;
+}
+
+ItemRec item_of(const cx_expert_desc& q, int pb, int np) {
+    return ItemRec{q.w_up, q.w_gate, q.w_down, q.s_up, q.s_gate, q.s_down, pb, np, 128, 128, 128, 0, {0, 0, 0, 0}};
+}
+
+// Average single-launch time (us) of `n` launches issued back to back, each
+// bracketed by its own start/stop events (the launcher's LaunchTimer).
+template <class F>
+double time_launches(int n, F fn) {
+    for (int i = 0; i < 2; ++i) fn(i);
+    KB_CHECK(hipDeviceSynchronize());
+    std::vector<LaunchTimer> t(n);
+    for (auto& x : t) {
+        KB_CHECK(hipEventCreate(&x.start));
+        KB_CHECK(hipEventCreate(&x.stop));
+    }
+    for (int i = 0; i < n; ++i) {
+        current_launch_timer() = &t[i];
+        fn(i);
+    }
+    current_launch_timer() = nullptr;
+    KB_CHECK(hipDeviceSynchronize());
+    double sum = 0;
+    for (auto& x : t) {
+        float ms = 0;
+        KB_CHECK(hipEventElapsedTime(&ms, x.start, x.stop));
+        sum += ms * 1e3;
+        (void)hipEventDestroy(x.start);
+        (void)hipEventDestroy(x.stop);
+    }
+    return sum / n;
+}
+
+void report(const char* what, double us, double bytes) {
+    std::printf("  %-58s %9.2f us  %6.2f TB/s\n", what, us, bytes / us * 1e-6);
+    std::fflush(stdout);
+}
+
+// ---------------------------------------------------------------------------
+// One-token decode plans: 8 routed experts + the shared expert (pairs: shared
+// 0, routed 1..8, as the decode planner numbers them).
+struct DecodePlans {
+    std::vector<PlanPtrs> plans;
+    std::vector<cx_expert_desc> shared;
+    float* topk_w = nullptr;
+    uint16_t *x = nullptr, *h_hi = nullptr, *h_lo = nullptr, *y = nullptr;
+    float* y_part = nullptr;
+    DecodePlans(const Pool& pool, int n_plans, uint32_t seed) {
+        std::mt19937 rng(seed);
+        const int n_exp = (int)pool.d.size();
+        for (int pi = 0; pi < n_plans; ++pi) {
+            std::vector<int> pick;
+            while ((int)pick.size() < 9) {
+                const int e = rng() % n_exp;
+                if (std::find(pick.begin(), pick.end(), e) == pick.end()) pick.push_back(e);
+            }
+            std::sort(pick.begin(), pick.begin() + 8);
+            std::vector<ItemRec> rec;
+            for (int i = 0; i < 8; ++i) rec.push_back(item_of(pool.d[pick[i]], 1 + i, 1));
+            rec.push_back(item_of(pool.d[pick[8]], 0, 1));
+            PlanPtrs P{};
+            PlanHdr h{};
+            h.n_slots = h.n_items = h.n_pairs = 9;
+            h.n_routed_slots = h.n_routed_items = 8;
+            P.hdr = dev_copy(std::vector<PlanHdr>{h});
+            P.item_rec = dev_copy(rec);
+            P.token_pairs = dev_copy(std::vector<int>{1, 2, 3, 4, 5, 6, 7, 8, 0});
+            P.pair_row = dev_copy(std::vector<int>{0, 1, 2, 3, 4, 5, 6, 7, 8});
+            plans.push_back(P);
+            shared.push_back(pool.d[pick[8]]);
+        }
+        topk_w = dev_copy(std::vector<float>{0.3f, 0.25f, 0.2f, 0.4f, 0.35f, 0.3f, 0.4f, 0.3f});
+        KB_CHECK(hipMalloc(&x, kH * 2));
+        KB_CHECK(hipMalloc(&h_hi, 16 * kI * 2));
+        KB_CHECK(hipMalloc(&h_lo, 16 * kI * 2));
+        KB_CHECK(hipMalloc(&y, kH * 2));
+        KB_CHECK(hipMalloc(&y_part, 16 * (size_t)kH * 4));
+        k_fill_bytes<<<16, 256>>>((uint32_t*)x, kH / 2, 7);
+        k_fill_bytes<<<64, 256>>>((uint32_t*)h_hi, 16 * kI / 2, 9);
+        k_fill_bytes<<<64, 256>>>((uint32_t*)h_lo, 16 * kI / 2, 10);
+        KB_CHECK(hipDeviceSynchronize());
+    }
+    ExpertLaunch launch(int pi, const cx_expert_desc* table, int max_lds) const {
+        ExpertLaunch L{};
+        L.table = table;
+        L.plan = plans[pi % plans.size()];
+        L.max_items = 8;
+        L.n_tokens = 1;
+        L.hidden = kH;
+        L.inter = kI;
+        L.maxt = 1;
+        L.x = x;
+        L.in_dtype = CX_DTYPE_BF16;
+        L.h_hi = h_hi;
+        L.h_lo = h_lo;
+        L.y_part = y_part;
+        L.y = y;
+        L.out_dtype = CX_DTYPE_BF16;
+        L.np_lds = 1;
+        L.skip_shared = 1;
+        L.max_lds = max_lds;
+        return L;
+    }
+};
+
+int max_lds() {
+    int v = 0;
+    KB_CHECK(hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, 0));
+    return v;
+}
+
+// Bare stream of the one-token down's bytes (no compute): 9 matrices, the
+// k_down_item shape (workgroup = one item x 64 rows, full-K waves) or the
+// k_down_comb1 shape (workgroup = 16 rows x all items: wave w = item w's 16
+// k-blocks then 2 k-blocks of the shared expert, one 8-deep ring).
+struct DownPtrs {
+    const uint8_t* m[9];
+};
+
+__device__ __forceinline__ uint32_t fold(const u32x4 (&w)[2]) {
+    return w[0][0] + w[0][1] * 3u + w[0][2] * 5u + w[0][3] * 7u + w[1][0] * 11u + w[1][1] * 13u + w[1][2] + w[1][3];
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_bare_down_item(DownPtrs P, uint32_t* sink) {
+    constexpr int NKB = 16, D = 6;
+    const int wave = wave_id(), lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+    const uint8_t* p = P.m[blockIdx.y] + (size_t)(blockIdx.x * 64 + wave * 16 + c) * kI + g * 32;
+    u32x4 wb[D][2];
+    uint32_t acc = 0;
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+        wb[s][0] = ld16(p + s * kKB);
+        wb[s][1] = ld16(p + s * kKB + 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < NKB; ++k) {
+        acc ^= fold(wb[k % D]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (k + D < NKB) {
+            wb[k % D][0] = ld16(p + (k + D) * kKB);
+            wb[k % D][1] = ld16(p + (k + D) * kKB + 16);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (acc == 0x12345678u) sink[threadIdx.x] = acc;
+}
+
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_bare_down_rows(DownPtrs P, uint32_t* sink) {
+    constexpr int NK = 18, D = 8;
+    const int wave = wave_id(), lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+    const size_t row = (size_t)(blockIdx.x * 16 + c) * kI;
+    const uint8_t* p = P.m[wave] + row + g * 32;
+    const uint8_t* q = P.m[8] + row + (size_t)(2 * wave) * kKB + g * 32;
+    auto at = [&](int k) { return k < 16 ? p + k * kKB : q + (k - 16) * kKB; };
+    u32x4 wb[D][2];
+    uint32_t acc = 0;
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+        wb[s][0] = ld16(at(s));
+        wb[s][1] = ld16(at(s) + 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+        acc ^= fold(wb[k % D]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (k + D < NK) {
+            wb[k % D][0] = ld16(at(k + D));
+            wb[k % D][1] = ld16(at(k + D) + 16);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (acc == 0x12345678u) sink[threadIdx.x] = acc;
+}
+
+int cmd_decode_down(int iters) {
+    std::printf("decode-down: one token, 8 routed + shared expert, experts spread over 24 x 2 GiB\n");
+    Pool pool(true);
+    DecodePlans dp(pool, 16, 3);
+    cx_expert_desc* table = dev_copy(pool.d);
+    uint32_t* sink = nullptr;
+    KB_CHECK(hipMalloc(&sink, 4096));
+    const int lds = max_lds();
+    const double down_bytes = 9.0 * (kMat + 56 * 16 * 4) + 2.0 * kH;
+    std::mt19937 rng(11);
+    std::vector<DownPtrs> sets(16);
+    for (auto& s : sets)
+        for (int j = 0; j < 9; ++j) s.m[j] = pool.d[rng() % pool.d.size()].w_down;
+    for (int rep = 0; rep < 2; ++rep) {
+        std::printf(" pass %d\n", rep + 1);
+        report("bare stream, k_down_item shape (item x 64 rows)",
+               time_launches(iters, [&](int i) {
+                   cx_launch(k_bare_down_item, dim3(112, 9), dim3(256), 0u, (hipStream_t)0, sets[i % 16], sink);
+               }), 9.0 * kMat);
+        report("bare stream, k_down_comb1 shape (16 rows x all items)",
+               time_launches(iters, [&](int i) {
+                   cx_launch(k_bare_down_rows, dim3(kH / 16), dim3(512), 0u, (hipStream_t)0, sets[i % 16], sink);
+               }), 9.0 * kMat);
+        report("k_down_comb1 (down + combine)", time_launches(iters, [&](int i) {
+                   ExpertLaunch L = dp.launch(i, table, lds);
+                   L.skip_shared = 0;
+                   L.max_items = 9;
+                   KB_CHECK(launch_down_comb1(L, L.plan.token_pairs, dp.topk_w, 8, 0));
+               }), down_bytes);
+        report("k_down_item (down, 9 items)", time_launches(iters, [&](int i) {
+                   ExpertLaunch L = dp.launch(i, table, lds);
+                   L.skip_shared = 0;
+                   L.max_items = 9;
+                   KB_CHECK(launch_down(L, 0));
+               }), down_bytes);
+        report("k_combine_dec (combine)", time_launches(iters, [&](int i) {
+                   ExpertLaunch L = dp.launch(i, table, lds);
+                   KB_CHECK(launch_combine_dec(L.plan, dp.topk_w, L.y_part, 1, 8, 1, kH, L.y, CX_DTYPE_BF16,
+                                               nullptr, 0));
+               }), 9.0 * kH * 4);
+    }
+    return 0;
+}
+
+int cmd_placement(int iters) {
+    for (int spread = 0; spread < 2; ++spread) {
+        Pool pool(spread == 1);
+        std::printf("placement: %s (%zu experts)\n", spread ? "24 x 2 GiB chunks" : "one 2.1 GB buffer",
+                    pool.d.size());
+        DecodePlans dp(pool, 16, 3);
+        cx_expert_desc* table = dev_copy(pool.d);
+        const int lds = max_lds();
+        const double gu_bytes = 8.0 * (2 * kMat + 2 * 16 * 56 * 4) + kH * 2;
+        const double down_bytes = 9.0 * (kMat + 56 * 16 * 4) + 2.0 * kH;
+        report("k_gate_up_t (8 routed experts)", time_launches(iters, [&](int i) {
+                   KB_CHECK(launch_gate_up(dp.launch(i, table, lds), 0));
+               }), gu_bytes);
+        report("k_down_comb1 (8 routed + shared, combine)", time_launches(iters, [&](int i) {
+                   ExpertLaunch L = dp.launch(i, table, lds);
+                   L.skip_shared = 0;
+                   L.max_items = 9;
+                   KB_CHECK(launch_down_comb1(L, L.plan.token_pairs, dp.topk_w, 8, 0));
+               }), down_bytes);
+        (void)hipFree(table);
+    }
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Config-3-like prefill plan: 512 tokens, 256 routed experts whose pair counts
+// follow 1 + 12 rank^-1.1 (sum 4096, max ~170), plus the shared expert's 512
+// pairs; items of <= 64 pairs as the general planner cuts them.
+struct PrefillPlan {
+    ExpertLaunch L{};
+    int n_items = 0, n_routed_items = 0;
+    int tiles[5] = {0, 0, 0, 0, 0};
+    PrefillPlan(const Pool& pool, uint32_t seed) {
+        const int T = 512, E = 256, P = T * 8 + T;
+        std::mt19937 rng(seed);
+        std::vector<int> perm(E);
+        for (int e = 0; e < E; ++e) perm[e] = e;
+        std::shuffle(perm.begin(), perm.end(), rng);
+        std::vector<double> wgt(E);
+        double sum = 0;
+        for (int r = 0; r < E; ++r) {
+            wgt[perm[r]] = 1.0 + 12.0 * std::pow(r + 1, -1.1);
+            sum += wgt[perm[r]];
+        }
+        std::vector<int> cnt(E);
+        int tot = 0;
+        for (int e = 0; e < E; ++e) {
+            cnt[e] = std::max(1, (int)std::floor(4096 * wgt[e] / sum));
+            tot += cnt[e];
+        }
+        for (int e = 0; tot < 4096; e = (e + 1) % E, ++tot) cnt[e]++;
+        std::vector<int> pick;
+        while ((int)pick.size() < E + 1) {
+            const int e = rng() % pool.d.size();
+            if (std::find(pick.begin(), pick.end(), e) == pick.end()) pick.push_back(e);
+        }
+        std::vector<ItemRec> items;
+        std::vector<int> ptok(P);
+        int p = T;
+        for (int e = 0; e < E; ++e) {
+            for (int o = 0; o < cnt[e]; o += 64) {
+                const int np = std::min(64, cnt[e] - o);
+                items.push_back(item_of(pool.d[pick[e]], p + o, np));
+                tiles[(np + 15) / 16]++;
+            }
+            for (int j = 0; j < cnt[e]; ++j) ptok[p + j] = rng() % T;
+            p += cnt[e];
+        }
+        n_routed_items = (int)items.size();
+        for (int o = 0; o < T; o += 64) items.push_back(item_of(pool.d[pick[E]], o, 64));
+        for (int t = 0; t < T; ++t) ptok[t] = t;
+        n_items = (int)items.size();
+        PlanHdr h{};
+        h.n_slots = E + 1;
+        h.n_items = n_items;
+        h.n_pairs = P;
+        h.n_routed_slots = E;
+        h.n_routed_items = n_routed_items;
+        PlanPtrs PP{};
+        PP.hdr = dev_copy(std::vector<PlanHdr>{h});
+        PP.item_rec = dev_copy(items);
+        PP.pair_token = dev_copy(ptok);
+        uint16_t *x = nullptr, *hh = nullptr, *hl = nullptr;
+        float* yp = nullptr;
+        KB_CHECK(hipMalloc(&x, (size_t)T * kH * 2));
+        KB_CHECK(hipMalloc(&hh, (size_t)P * kI * 2));
+        KB_CHECK(hipMalloc(&hl, (size_t)P * kI * 2));
+        KB_CHECK(hipMalloc(&yp, (size_t)P * kH * 4));
+        k_fill_bytes<<<1024, 256>>>((uint32_t*)x, (size_t)T * kH / 2, 7);
+        k_fill_bytes<<<1024, 256>>>((uint32_t*)hh, (size_t)P * kI / 2, 9);
+        k_fill_bytes<<<1024, 256>>>((uint32_t*)hl, (size_t)P * kI / 2, 10);
+        L.table = dev_copy(pool.d);  // grouped mode (the grouped kernels read the plan's records)
+        L.plan = PP;
+        L.max_items = n_items;
+        L.n_tokens = T;
+        L.hidden = kH;
+        L.inter = kI;
+        L.maxt = 4;
+        L.x = x;
+        L.in_dtype = CX_DTYPE_BF16;
+        L.h_hi = hh;
+        L.h_lo = hl;
+        L.y_part = yp;
+        L.out_dtype = CX_DTYPE_BF16;
+        L.max_lds = max_lds();
+        KB_CHECK(hipDeviceSynchronize());
+    }
+};
+
+// Bare streams over a prefill plan's gate/up bytes.  ORDER 0: the grouped
+// kernel's pattern (128-row workgroups, wave = 16 rows x full K, row-major
+// bytes); ORDER 1: 16-row workgroups, wave = 16 rows x K/4 (the decode
+// gate/up's pattern); ORDER 2: 128-row workgroups, full-K waves, reading the
+// same bytes in tiled order ([16-row group][k-block][16 rows x 128 B]
+// contiguous), the order a re-layout at upload would store.
+template <int ORDER>
+__global__ __launch_bounds__(512) void k_bare_gu(ExpertLaunch L, uint32_t* sink) {
+    constexpr int TILES = ORDER == 1 ? kI / 16 : kI / 128;
+    const int tile = blockIdx.x % TILES, item = blockIdx.x / TILES;
+    const int wave = wave_id(), lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+    if (ORDER == 1 && wave >= 4) return;
+    const ItemRec r = ld_uniform(L.plan.item_rec + item);
+    constexpr int NKB = ORDER == 1 ? 14 : 56, D = 4;
+    const int rg = ORDER == 1 ? tile : tile * 8 + wave;  // 16-row group
+    const int kb0 = ORDER == 1 ? wave * 14 : 0;
+    auto at = [&](const uint8_t* m, int k) -> const uint8_t* {
+        if (ORDER == 2) return m + ((size_t)rg * 56 + k) * 2048 + (size_t)lane * 32;
+        return m + (size_t)(rg * 16 + c) * kH + (size_t)(kb0 + k) * kKB + g * 32;
+    };
+    u32x4 wb[D][4];
+    uint32_t acc = 0;
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+        wb[s][0] = ld16(at(r.w_gate, s));
+        wb[s][1] = ld16(at(r.w_gate, s) + 16);
+        wb[s][2] = ld16(at(r.w_up, s));
+        wb[s][3] = ld16(at(r.w_up, s) + 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll 4
+    for (int k = 0; k < NKB; ++k) {
+        const int s = k % D;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc ^= wb[s][j][0] + wb[s][j][1] * 3u + wb[s][j][2] * 5u + wb[s][j][3] * 7u;
+        if (k + D < NKB) {
+            __builtin_amdgcn_sched_barrier(0);
+            wb[s][0] = ld16(at(r.w_gate, k + D));
+            wb[s][1] = ld16(at(r.w_gate, k + D) + 16);
+            wb[s][2] = ld16(at(r.w_up, k + D));
+            wb[s][3] = ld16(at(r.w_up, k + D) + 16);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    if (acc == 0x12345678u) sink[threadIdx.x] = acc;
+}
+
+int cmd_layout(int iters) {
+    Pool pool(true);
+    std::vector<PrefillPlan> plans;
+    for (int l = 0; l < 4; ++l) plans.emplace_back(pool, 5 + l);
+    const PrefillPlan& p0 = plans[0];
+    std::printf("layout: config-3-like plan, %d items (%d routed; column tiles 1:%d 2:%d 3:%d 4:%d), "
+                "experts spread over 24 x 2 GiB\n",
+                p0.n_items, p0.n_routed_items, p0.tiles[1], p0.tiles[2], p0.tiles[3], p0.tiles[4]);
+    uint32_t* sink = nullptr;
+    KB_CHECK(hipMalloc(&sink, 4096));
+    const double bytes = 257.0 * 2 * kMat;
+    for (int rep = 0; rep < 2; ++rep) {
+        std::printf(" pass %d\n", rep + 1);
+        report("natural order, 128-row workgroups, full-K waves", time_launches(iters, [&](int i) {
+                   const PrefillPlan& p = plans[i % 4];
+                   cx_launch(k_bare_gu<0>, dim3(16 * p.n_items), dim3(512), 0u, (hipStream_t)0, p.L, sink);
+               }), bytes);
+        report("natural order, 16-row workgroups, K/4 waves", time_launches(iters, [&](int i) {
+                   const PrefillPlan& p = plans[i % 4];
+                   cx_launch(k_bare_gu<1>, dim3(128 * p.n_items), dim3(256), 0u, (hipStream_t)0, p.L, sink);
+               }), bytes);
+        report("tiled order (re-layout at upload), 128-row workgroups", time_launches(iters, [&](int i) {
+                   const PrefillPlan& p = plans[i % 4];
+                   cx_launch(k_bare_gu<2>, dim3(16 * p.n_items), dim3(512), 0u, (hipStream_t)0, p.L, sink);
+               }), bytes);
+        report("k_gu_grp (the kernel, natural order)", time_launches(iters, [&](int i) {
+                   KB_CHECK(launch_gate_up(plans[i % 4].L, 0));
+               }), bytes + 512.0 * kH * 2);
+    }
+    return 0;
+}
+
+int cmd_grouped(int iters) {
+    Pool pool(true);
+    std::vector<PrefillPlan> plans;
+    for (int l = 0; l < 4; ++l) plans.emplace_back(pool, 5 + l);
+    std::printf("grouped: config-3-like plan, %d items, experts spread over 24 x 2 GiB\n", plans[0].n_items);
+    const double gu = 257.0 * 2 * kMat + 512.0 * kH * 2;
+    const double dn = 257.0 * kMat + 4608.0 * kH * 4;
+    for (int rep = 0; rep < 2; ++rep) {
+        report("k_gu_grp", time_launches(iters, [&](int i) { KB_CHECK(launch_gate_up(plans[i % 4].L, 0)); }), gu);
+        report("k_dn_grp", time_launches(iters, [&](int i) { KB_CHECK(launch_down(plans[i % 4].L, 0)); }), dn);
+    }
+    return 0;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    const char* cmd = argc > 1 ? argv[1] : "";
+    const int iters = argc > 2 ? std::max(4, std::atoi(argv[2])) : 30;
+    if (!std::strcmp(cmd, "layout")) return cmd_layout(std::min(iters, 12));
+    if (!std::strcmp(cmd, "decode-down")) return cmd_decode_down(iters);
+    if (!std::strcmp(cmd, "placement")) return cmd_placement(iters);
+    if (!std::strcmp(cmd, "grouped")) return cmd_grouped(std::min(iters, 12));
+    std::fprintf(stderr, "usage: cx_kbench layout|decode-down|placement|grouped [launches]\n");
+    return 2;
+}
