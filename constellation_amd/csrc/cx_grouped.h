@@ -254,12 +254,166 @@ __device__ __forceinline__ void grp_gate_up_item(const ExpertLaunch& L, const Un
     }
 }
 
+// gate/up of a one-tile item (<= 16 pairs) with the x rows staged in LDS a
+// chunk of kGuChunk k-blocks at a time (two chunk buffers): the next chunk is
+// loaded into registers while the current one is consumed and published with
+// one barrier per chunk, so the k-block steps issue weight loads only.  The
+// whole K loop is unrolled (every load is an ordinary register load, so the
+// compiler's waits stay exact).  LDS: grp_gu_c1_lds().
+constexpr int kGuChunk = 14;
+constexpr size_t kGuChunkBytes = (size_t)kGuChunk * kActBlk;  // 56 KB
+constexpr size_t grp_gu_c1_lds() { return 2 * kGuChunkBytes; }
+
 template <int NKB, bool F16, bool SINGLE>
+__device__ __forceinline__ void grp_gate_up_item_c1(const ExpertLaunch& L, const Unit& u, int tile,
+                                                    unsigned char* lds) {
+    typedef Mma<F16> M;
+    typedef typename M::V V;
+    static_assert(NKB % kGuChunk == 0 && NKB <= 64, "whole chunks; scale row one k-block per lane");
+    static_assert(kGuGrpWaves == 8, "chunk loader: 512 threads x 7 pieces = 14 k-blocks");
+    constexpr int D = kGuGrpD, NCH = NKB / kGuChunk, XL = kGuChunk / 2;  // x loads per thread and chunk
+    const int H = u.e.hidden, I = u.e.inter;
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int g = lane >> 4, c = lane & 15;
+    const int r0 = tile * kGuGrpRows + wave * kTileRows;
+    const size_t roff = (size_t)(r0 + c) * H + g * 32;
+    const uint8_t* pg = u.e.w_gate + roff;
+    const uint8_t* pu = u.e.w_up + roff;
+    const int rbg = __builtin_amdgcn_readfirstlane(r0 / u.e.gate_rb);
+    const int rbu = __builtin_amdgcn_readfirstlane(r0 / u.e.up_rb);
+    float scg_v = lane < NKB ? ldf(u.e.s_gate + (size_t)rbg * NKB + lane) : 0.f;
+    float scu_v = lane < NKB ? ldf(u.e.s_up + (size_t)rbu * NKB + lane) : 0.f;
+    // chunk loader: thread (wave w, lane (c, g)) carries piece j = w % 4 of
+    // k-blocks w / 4 + 2i (i < 7) of the chunk for pair c: 16 B each
+    const int q = min(c, u.np - 1);
+    const int tok = SINGLE ? u.pb + q : ldi(L.plan.pair_token + u.pb + q);
+    const int pj = wave & 3, kq = wave >> 2;
+    const uint16_t* xs = static_cast<const uint16_t*>(L.x) + (size_t)tok * H + 8 * (4 * g + pj);
+    unsigned char* xdst = lds + pj * kPiece + lane * 16;
+    u32x4 xr[XL];
+    // chunk loads from a base advanced per chunk (kept opaque so the offsets
+    // stay immediates instead of one precomputed address per load)
+    const uint16_t* xb = xs + (size_t)kq * kKB;
+    auto load_chunk = [&](int ch) {
+        if (ch > 0) {
+            xb += (size_t)kGuChunk * kKB;
+            asm volatile("" : "+v"(xb));
+        }
+#pragma unroll
+        for (int i = 0; i < XL; ++i) xr[i] = ld16(xb + (size_t)(2 * i) * kKB);
+    };
+    auto store_chunk = [&](int ch) {
+        unsigned char* dst = xdst + (size_t)(ch & 1) * kGuChunkBytes;
+#pragma unroll
+        for (int i = 0; i < XL; ++i) *reinterpret_cast<u32x4*>(dst + (size_t)(kq + 2 * i) * kActBlk) = xr[i];
+    };
+    u32x4 wb[D][4];
+    // weight loads relative to the current chunk's base (kb = first k-block)
+    const uint8_t* pgb = pg;
+    const uint8_t* pub = pu;
+    auto issue = [&](int k, int kb) {
+        const int st = k % D;
+        const size_t o = (size_t)(k - kb) * kKB;
+        wb[st][0] = ld16(pgb + o);
+        wb[st][1] = ld16(pgb + o + 16);
+        wb[st][2] = ld16(pub + o);
+        wb[st][3] = ld16(pub + o + 16);
+    };
+    // chunk 0 first, then the weight prologue, then chunk 0 into LDS and
+    // chunk 1 behind the weights
+    load_chunk(0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < D && k < NKB; ++k) {
+        issue(k, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    store_chunk(0);
+    if (NCH > 1) load_chunk(1);
+    asm volatile("" : "+v"(scg_v), "+v"(scu_v));
+    lds_write_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+        const unsigned char* src = lds + (size_t)(ch & 1) * kGuChunkBytes + lane * 16;
+        if (ch > 0) {
+            pgb += (size_t)kGuChunk * kKB;
+            pub += (size_t)kGuChunk * kKB;
+            asm volatile("" : "+v"(pgb), "+v"(pub));
+        }
+#pragma unroll
+        for (int kk = 0; kk < kGuChunk; ++kk) {
+            const int k = ch * kGuChunk + kk, st = k % D;
+            const float sgk = lane_scale(scg_v, k), suk = lane_scale(scu_v, k);
+            V ag[4], au[4], bx[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                ag[j] = M::cvt(wb[st][j >> 1][(j & 1) * 2], wb[st][j >> 1][(j & 1) * 2 + 1]);
+                au[j] = M::cvt(wb[st][2 + (j >> 1)][(j & 1) * 2], wb[st][2 + (j >> 1)][(j & 1) * 2 + 1]);
+                bx[j] = M::bits(*reinterpret_cast<const u32x4*>(src + (size_t)kk * kActBlk + j * kPiece));
+            }
+            f32x4 tg = M::mma(ag[0], bx[0], zero);
+            f32x4 tu = M::mma(au[0], bx[0], zero);
+#pragma unroll
+            for (int j = 1; j < 4; ++j) {
+                tg = M::mma(ag[j], bx[j], tg);
+                tu = M::mma(au[j], bx[j], tu);
+            }
+            accg += sgk * tg;
+            accu += suk * tu;
+            // keep the scaled accumulate at this step (left free, the
+            // compiler defers it and holds every step's product)
+            asm volatile("" : "+v"(accg), "+v"(accu));
+            __builtin_amdgcn_sched_barrier(0);
+            if (k + D < NKB) issue(k + D, ch * kGuChunk);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (ch + 1 < NCH) {
+            // chunk ch + 1 into the buffer chunk ch - 1 used (every wave has
+            // passed the barrier after its last read), chunk ch + 2 behind
+            store_chunk(ch + 1);
+            if (ch + 2 < NCH) load_chunk(ch + 2);
+            lds_write_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    if (c < u.np) {
+        const size_t p = (size_t)(u.pb + c);
+        const float wf = !SINGLE && L.fold_weight ? L.plan.pair_weight[p] : 1.0f;
+        const int row = r0 + 4 * g;
+        uint32_t hi[4], lo[4];
+        float hv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float gate = accg[i], up = accu[i];
+            const float h = (gate / (1.0f + expf(-gate))) * up;
+            hv[i] = h;
+            const float hw = h * wf;
+            hi[i] = bf16_rne(hw);
+            lo[i] = bf16_rne(hw - __uint_as_float(hi[i] << 16));
+        }
+        *reinterpret_cast<uint2*>(L.h_hi + p * I + row) = uint2{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
+        *reinterpret_cast<uint2*>(L.h_lo + p * I + row) = uint2{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
+        if (L.h_f32 != nullptr)
+            *reinterpret_cast<float4*>(L.h_f32 + p * I + row) = float4{hv[0], hv[1], hv[2], hv[3]};
+    }
+}
+
+// C1: one-tile items take the chunked path (needs grp_gu_c1_lds() of LDS).
+template <int NKB, bool F16, bool SINGLE, bool C1 = false>
 __device__ __forceinline__ void grp_gate_up_tile(const ExpertLaunch& L, int tile, int item,
                                                  unsigned char* lds) {
     Unit u;
     if (!resolve_unit<SINGLE>(L, item, kGrpPairs, &u)) return;
     const int nt = (u.np + kTileTok - 1) / kTileTok;  // uniform: one branch per item
+    if constexpr (C1) {
+        if (nt == 1) {
+            grp_gate_up_item_c1<NKB, F16, SINGLE>(L, u, tile, lds);
+            return;
+        }
+    }
     if (nt == 1) grp_gate_up_item<NKB, 1, F16, SINGLE>(L, u, tile, lds);
     else if (nt == 2) grp_gate_up_item<NKB, 2, F16, SINGLE>(L, u, tile, lds);
     else if (nt == 3) grp_gate_up_item<NKB, 3, F16, SINGLE>(L, u, tile, lds);

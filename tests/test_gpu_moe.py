@@ -557,19 +557,21 @@ def test_device_probe_invariants(gpu):
     assert info["capability_flags"] & 0x7 == 0x7
 
 
-def test_full_size_prefill_grouped_items(gpu, oracle):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_full_size_prefill_grouped_items(gpu, oracle, dtype):
     """The grouped GEMM at DeepSeek-V3 shapes (H=7168, I=2048) with items of
     every width: expert 0 takes all 72 tokens (items of 64 + 8 pairs), expert 1
-    40 (3 column tiles), expert 2 20 (2 tiles), the rest a few each; shared
-    expert on.  The oracle checks a sample of tokens spread over the items."""
-    print("[moe] full-size prefill items", flush=True)
+    40 (3 column tiles), expert 2 20 (2 tiles), the rest a few each (one-tile
+    items, which stage x in LDS chunks); shared expert on.  bf16 and fp16
+    activations; the oracle checks a sample of tokens spread over the items."""
+    print(f"[moe] full-size prefill items {dtype}", flush=True)
     E, H, I, T, K = 16, 7168, 2048, 72, 4
     from constellation_amd.engine import Expert, Layer
     experts = [Expert.generate(0, 91, 0x4000 + 4 * e) for e in range(E)]
     sh = Expert.generate(0, 91, 0x4000 + 4 * E)
     layer = Layer(gpu, experts, sh)
     try:
-        x = gpu.gen_normal(92, 1, (T, H), 1.0, torch.bfloat16)
+        x = gpu.gen_normal(92, 1, (T, H), 1.0, dtype)
         rng = np.random.default_rng(93)
         ids = np.full((T, K), -1, np.int32)
         for t in range(T):
@@ -593,7 +595,7 @@ def test_full_size_prefill_grouped_items(gpu, oracle):
         yf = yf.cpu().numpy()[sel]
         assert rel_l2(yf, ref) < 1e-5, rel_l2(yf, ref)
         assert np.abs(yf - ref).max() < 2e-2
-        assert np.array_equal(_bits(y)[sel], oracle.encode_act(yf, BF16, "rne"))
+        assert np.array_equal(_bits(y)[sel], oracle.encode_act(yf, BF16 if dtype == torch.bfloat16 else FP16, "rne"))
     finally:
         _free(layer, experts, sh)
 
