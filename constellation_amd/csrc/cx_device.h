@@ -154,4 +154,18 @@ __device__ __forceinline__ void store_out4(void* y, float* y_f32, size_t idx, f3
     if (y_f32 != nullptr) *reinterpret_cast<float4*>(y_f32 + idx) = float4{v[0], v[1], v[2], v[3]};
 }
 
+// The first n (<= 4) of four consecutive output rows, one element at a time
+// (idx need not be a multiple of 4).
+__device__ __forceinline__ void store_out_n(void* y, float* y_f32, size_t idx, f32x4 v, int n,
+                                            int out_dtype) {
+    uint16_t* yo = static_cast<uint16_t*>(y) + idx;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (i < n) {
+            yo[i] = (uint16_t)cast_out(v[i], out_dtype);
+            if (y_f32 != nullptr) y_f32[idx + i] = v[i];
+        }
+    }
+}
+
 }  // namespace cx

@@ -158,8 +158,8 @@ namespace cx {
 
 // ---------------------------------------------------------------------------
 // One-token decode: down projection of every item and the weighted combine in
-// one launch.  Workgroup = 16 output rows x all items: wave w streams routed
-// item w's 16 rows over the full K (NKB k-blocks), then its share (NKS
+// one launch.  Workgroup = a tile of <= 16 output rows x all items: wave w
+// streams routed item w's rows over the full K (NKB k-blocks), then its share (NKS
 // k-blocks) of the shared expert's K, as one weight ring; the h rows it needs
 // (routed item: all of K; shared expert: its k range) are DMA'd into the
 // wave's own LDS slice first.  The output rows are then combined in LDS —
@@ -184,11 +184,33 @@ struct Dc1Geom {
     static constexpr int kLds = kRedOff + 2 * kDc1Waves * 4 * 16;      // + routed / shared row partials
 };
 
-// One wave's ring: NR routed stages (item weights pd, scales scd) then NS
-// shared stages (ps, scs); h of stage k read from the wave's LDS slice.
+// Scale rows of one item for a tile of output rows: rows of the tile at or
+// past `split` (tile-relative) lie in the next row block.  Row blocks are
+// multiples of 16 rows and tiles at most 16, so a tile spans at most two.
+struct Dc1Scales {
+    const float* lo;
+    const float* hi;
+    int split;
+};
+
+__device__ __forceinline__ Dc1Scales dc1_scales(const float* s_down, int down_rb, int r0, int rows,
+                                                int nkb, int k0) {
+    const int rb = __builtin_amdgcn_readfirstlane(r0 / down_rb);
+    const int split = (rb + 1) * down_rb - r0;
+    Dc1Scales q;
+    q.lo = s_down + (size_t)rb * nkb + k0;
+    q.hi = split < rows ? q.lo + nkb : q.lo;
+    q.split = split;
+    return q;
+}
+
+// One wave's ring: NR routed stages (item weights pd, scales qd) then NS
+// shared stages (ps, qs); h of stage k read from the wave's LDS slice.  The
+// lane holds output rows 4g..4g+3 of the tile; each takes its own row
+// block's scale.
 template <int NR, int NS, int D, int NKB>
-__device__ __forceinline__ void dc1_ring(const uint8_t* pd, const uint8_t* ps, const float* scd,
-                                         const float* scs, const unsigned char* hw, int g,
+__device__ __forceinline__ void dc1_ring(const uint8_t* pd, const uint8_t* ps, Dc1Scales qd,
+                                         Dc1Scales qs, const unsigned char* hw, int g,
                                          f32x4* acc_r, f32x4* acc_s) {
     typedef Dc1Geom<NKB> G;
     constexpr int NK = NR + NS;
@@ -203,9 +225,18 @@ __device__ __forceinline__ void dc1_ring(const uint8_t* pd, const uint8_t* ps, c
         wb[s][1] = ld16(wptr(s) + 16);
     }
     __builtin_amdgcn_sched_barrier(0);
-    float sc[NK];
+    float sc[NK], sc_hi[NK];
 #pragma unroll
-    for (int k = 0; k < NK; ++k) sc[k] = k < NR ? ldsc(scd + k) : ldsc(scs + (k - NR));
+    for (int k = 0; k < NK; ++k) {
+        sc[k] = k < NR ? ldsc(qd.lo + k) : ldsc(qs.lo + (k - NR));
+        sc_hi[k] = k < NR ? ldsc(qd.hi + k) : ldsc(qs.hi + (k - NR));
+    }
+    bool hi_r[4], hi_s[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        hi_r[i] = 4 * g + i >= qd.split;
+        hi_s[i] = 4 * g + i >= qs.split;
+    }
     // the DMA'd h is older than the ring's loads; nothing of the loop may
     // move above this wait (the compiler cannot count LDS DMA exactly and
     // would drain the ring with vmcnt(0))
@@ -225,8 +256,11 @@ __device__ __forceinline__ void dc1_ring(const uint8_t* pd, const uint8_t* ps, c
             hb[4 + j] = *reinterpret_cast<const u32x4*>(hp + lo + 16 * j);
         }
         const f32x4 t = down_step(wb[s], hb);
-        if (k < NR) ar += sc[k] * t;
-        else as += sc[k] * t;
+        f32x4 sv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = (k < NR ? hi_r[i] : hi_s[i]) ? sc_hi[k] : sc[k];
+        if (k < NR) ar += sv * t;
+        else as += sv * t;
         __builtin_amdgcn_sched_barrier(0);
         if (k + D < NK) {
             wb[s][0] = ld16(wptr(k + D));
@@ -238,19 +272,22 @@ __device__ __forceinline__ void dc1_ring(const uint8_t* pd, const uint8_t* ps, c
     *acc_s = as;
 }
 
-// Row tile `rtile` (16 output rows).  The plan header and the wave's item
-// record come first, then the h DMA and the ring.  Wave 0 fetches the route
-// table with the DMA, so the combine needs no memory round trip.
+// Row tile `rtile` of `rows` (<= 16) output rows.  The plan header and the
+// wave's item record come first, then the h DMA and the ring.  Wave 0
+// fetches the route table with the DMA, so the combine needs no memory
+// round trip.  With rows < 16, the MFMA's spare rows repeat the tile's last
+// weight row (the same addresses, so no extra bytes) and are not stored.
 template <int NKB, int D>
 __device__ __forceinline__ void down_comb1_tile(const ExpertLaunch& L, const int* token_pairs,
                                                 const float* topk_w, int top_k, unsigned char* lds,
-                                                int rtile) {
+                                                int rtile, int rows) {
     typedef Dc1Geom<NKB> G;
     constexpr int NKS = G::NKS;
     const int I = L.inter;
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int g = lane >> 4, c = lane & 15;
-    const int r0 = rtile * kTileRows;
+    const int r0 = rtile * rows;
+    const int wr = r0 + min(c, rows - 1);  // weight row of this lane
     const PlanHdr hd = ld_uniform(L.plan.hdr);
     const int ts = hd.n_routed_items;
     const bool shared = hd.n_items > ts;
@@ -259,8 +296,7 @@ __device__ __forceinline__ void down_comb1_tile(const ExpertLaunch& L, const int
     unsigned char* hw = lds + wave * G::kWaveBytes;
     const uint8_t* pd = nullptr;
     const uint8_t* ps = nullptr;
-    const float* scd = nullptr;
-    const float* scs = nullptr;
+    Dc1Scales qd{nullptr, nullptr, kTileRows}, qs{nullptr, nullptr, kTileRows};
     // 0) h into this wave's LDS slice (1 KB per wave instruction), before any weight load
     if (has_r) {
         const ItemRec ri = ld_uniform(L.plan.item_rec + wave);
@@ -271,8 +307,8 @@ __device__ __forceinline__ void down_comb1_tile(const ExpertLaunch& L, const int
             __builtin_amdgcn_global_load_lds(hh + j * 512, hw + j * 1024, 16, 0, 0);
             __builtin_amdgcn_global_load_lds(hl + j * 512, hw + G::kRoutedBytes + j * 1024, 16, 0, 0);
         }
-        pd = ri.w_down + (size_t)(r0 + c) * I + g * 32;
-        scd = ri.s_down + (size_t)__builtin_amdgcn_readfirstlane(r0 / ri.down_rb) * (I / kKB);
+        pd = ri.w_down + (size_t)wr * I + g * 32;
+        qd = dc1_scales(ri.s_down, ri.down_rb, r0, rows, I / kKB, 0);
     }
     if (has_s) {
         const ItemRec rs = ld_uniform(L.plan.item_rec + ts);
@@ -282,8 +318,8 @@ __device__ __forceinline__ void down_comb1_tile(const ExpertLaunch& L, const int
             const uint16_t* src = (lane < LPP ? L.h_hi : L.h_lo) + (size_t)rs.pb * I + k0 + (lane % LPP) * 8;
             __builtin_amdgcn_global_load_lds(src, hw + 2 * G::kRoutedBytes, 16, 0, 0);
         }
-        ps = rs.w_down + (size_t)(r0 + c) * I + k0 + g * 32;
-        scs = rs.s_down + (size_t)__builtin_amdgcn_readfirstlane(r0 / rs.down_rb) * (I / kKB) + wave * NKS;
+        ps = rs.w_down + (size_t)wr * I + k0 + g * 32;
+        qs = dc1_scales(rs.s_down, rs.down_rb, r0, rows, I / kKB, wave * NKS);
     }
     // wave 0: the route table (lane k: pair and weight of route k), issued
     // with the DMA so that the ring's first wait covers it
@@ -295,9 +331,9 @@ __device__ __forceinline__ void down_comb1_tile(const ExpertLaunch& L, const int
     }
     __builtin_amdgcn_sched_barrier(0);
     f32x4 ar, as;
-    if (has_r && has_s) dc1_ring<NKB, NKS, D, NKB>(pd, ps, scd, scs, hw, g, &ar, &as);
-    else if (has_r) dc1_ring<NKB, 0, D, NKB>(pd, ps, scd, scs, hw, g, &ar, &as);
-    else if (has_s) dc1_ring<0, NKS, D, NKB>(pd, ps, scd, scs, hw, g, &ar, &as);
+    if (has_r && has_s) dc1_ring<NKB, NKS, D, NKB>(pd, ps, qd, qs, hw, g, &ar, &as);
+    else if (has_r) dc1_ring<NKB, 0, D, NKB>(pd, ps, qd, qs, hw, g, &ar, &as);
+    else if (has_s) dc1_ring<0, NKS, D, NKB>(pd, ps, qd, qs, hw, g, &ar, &as);
     else {
         lds_dma_barrier();
         ar = as = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -322,7 +358,10 @@ __device__ __forceinline__ void down_comb1_tile(const ExpertLaunch& L, const int
 #pragma unroll
             for (int w = 0; w < kDc1Waves; ++w) sum += red_s[w * 4 + (lane & 3)];
         }
-        if (lane < 4) store_out4(L.y, L.y_f32, (size_t)r0 + 4 * lane, sum, L.out_dtype);
+        if (lane < 4 && 4 * lane < rows) {
+            if (rows % 4 == 0) store_out4(L.y, L.y_f32, (size_t)r0 + 4 * lane, sum, L.out_dtype);
+            else store_out_n(L.y, L.y_f32, (size_t)r0 + 4 * lane, sum, min(4, rows - 4 * lane), L.out_dtype);
+        }
     }
 }
 

@@ -459,12 +459,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 
 // ---------------------------------------------------------------------------
 // One-token decode: down projection of every item plus the weighted combine
-// (down_comb1_tile, cx_down.h), grid = hidden/16 workgroups of 8 waves.
+// (down_comb1_tile, cx_down.h), grid = hidden/rows workgroups of 8 waves.
 template <int NKB, int D>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_down_comb1(
-    ExpertLaunch L, const int* __restrict__ token_pairs, const float* __restrict__ topk_w, int top_k) {
+    ExpertLaunch L, const int* __restrict__ token_pairs, const float* __restrict__ topk_w, int top_k,
+    int rows) {
     extern __shared__ __attribute__((aligned(16))) unsigned char dc_lds[];
-    down_comb1_tile<NKB, D>(L, token_pairs, topk_w, top_k, dc_lds, blockIdx.x);
+    down_comb1_tile<NKB, D>(L, token_pairs, topk_w, top_k, dc_lds, blockIdx.x, rows);
 }
 
 // ---------------------------------------------------------------------------
@@ -994,16 +995,30 @@ bool down_comb1_ok(int hidden, int inter, int top_k, int max_lds) {
            (size_t)max_lds >= lds;
 }
 
+// Rows per one-token down workgroup.  Two workgroups share a CU, and the
+// launch lasts as long as the CUs that stream the most rows: at hidden 7168
+// on 256 CUs, 448 tiles of 16 rows put two on 24 of the 32 CUs of each XCD
+// (32 rows) and one on the rest, while 512 tiles of 14 rows give every CU
+// two (28 rows).  Measured: 448 and 384 tiles of 16 rows take the same time,
+// 256 take 64 % of it.  14 is taken when it divides hidden and lowers the
+// busiest CU's rows.
+int down_comb1_rows(int hidden, int n_cu) {
+    auto busiest = [&](int r) { const int n = hidden / r; return (n + n_cu - 1) / n_cu * r; };
+    if (n_cu > 0 && hidden % 14 == 0 && busiest(14) < busiest(kTileRows)) return 14;
+    return kTileRows;
+}
+
 hipError_t launch_down_comb1(const ExpertLaunch& L, const int* token_pairs, const float* topk_w,
-                             int top_k, hipStream_t s) {
+                             int top_k, int n_cu, hipStream_t s) {
     if (L.table == nullptr || L.n_tokens != 1 || !down_comb1_ok(L.hidden, L.inter, top_k, L.max_lds))
         return hipErrorInvalidValue;
-    const dim3 grid(L.hidden / kTileRows), block(64 * kDc1Waves);
+    const int rows = down_comb1_rows(L.hidden, n_cu);
+    const dim3 grid(L.hidden / rows), block(64 * kDc1Waves);
     const size_t lds = down_comb1_lds(L.inter);
     switch (L.inter / kKB) {
-        case 16: cx_launch((k_down_comb1<16, kDc1Depth>), grid, block, lds, s, L, token_pairs, topk_w, top_k); break;
-        case 8: cx_launch((k_down_comb1<8, kDc1Depth>), grid, block, lds, s, L, token_pairs, topk_w, top_k); break;
-        default: cx_launch((k_down_comb1<4, 4>), grid, block, lds, s, L, token_pairs, topk_w, top_k); break;
+        case 16: cx_launch((k_down_comb1<16, kDc1Depth>), grid, block, lds, s, L, token_pairs, topk_w, top_k, rows); break;
+        case 8: cx_launch((k_down_comb1<8, kDc1Depth>), grid, block, lds, s, L, token_pairs, topk_w, top_k, rows); break;
+        default: cx_launch((k_down_comb1<4, 4>), grid, block, lds, s, L, token_pairs, topk_w, top_k, rows); break;
     }
     return hipGetLastError();
 }

@@ -264,14 +264,14 @@ constexpr int kGuChunk = 14;
 constexpr size_t kGuChunkBytes = (size_t)kGuChunk * kActBlk;  // 56 KB
 constexpr size_t grp_gu_c1_lds() { return 2 * kGuChunkBytes; }
 
-template <int NKB, bool F16, bool SINGLE>
+template <int NKB, bool F16, bool SINGLE, int D = kGuGrpD>
 __device__ __forceinline__ void grp_gate_up_item_c1(const ExpertLaunch& L, const Unit& u, int tile,
                                                     unsigned char* lds) {
     typedef Mma<F16> M;
     typedef typename M::V V;
     static_assert(NKB % kGuChunk == 0 && NKB <= 64, "whole chunks; scale row one k-block per lane");
     static_assert(kGuGrpWaves == 8, "chunk loader: 512 threads x 7 pieces = 14 k-blocks");
-    constexpr int D = kGuGrpD, NCH = NKB / kGuChunk, XL = kGuChunk / 2;  // x loads per thread and chunk
+    constexpr int NCH = NKB / kGuChunk, XL = kGuChunk / 2;  // x loads per thread and chunk
     const int H = u.e.hidden, I = u.e.inter;
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int g = lane >> 4, c = lane & 15;

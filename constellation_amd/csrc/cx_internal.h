@@ -162,11 +162,13 @@ hipError_t launch_combine_dec(const PlanPtrs& plan, const float* topk_w, const f
 // One-token decode (n_tokens == 1, decode plan): down of every item and the
 // weighted combine in one launch, writing y / y_f32 directly (no y_part).
 // Needs top_k <= 8, hidden % 16 == 0, inter / 128 in {4, 8, 16} and
-// down_comb1_lds(inter) bytes of LDS (L.max_lds).
+// down_comb1_lds(inter) bytes of LDS (L.max_lds).  Workgroups of
+// down_comb1_rows(hidden, n_cu) output rows (n_cu: the device's CUs).
 size_t down_comb1_lds(int inter);
 bool down_comb1_ok(int hidden, int inter, int top_k, int max_lds);
+int down_comb1_rows(int hidden, int n_cu);
 hipError_t launch_down_comb1(const ExpertLaunch& L, const int* token_pairs, const float* topk_w,
-                             int top_k, hipStream_t s);
+                             int top_k, int n_cu, hipStream_t s);
 hipError_t launch_plan(const int32_t* ids, const float* w, int n_tokens, int top_k,
                        const cx_expert_desc* table, int n_experts, int has_shared,
                        int item_cap, int max_items, PlanPtrs plan, int* err_flag,

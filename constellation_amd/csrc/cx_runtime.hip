@@ -230,6 +230,7 @@ struct cx_ctx {
     hipStream_t own_stream = nullptr;  // for the host-buffer entry point
     int* err_flag = nullptr;           // device int: error bits of the device checks
     int max_lds = 65536;               // dynamic LDS budget per workgroup
+    int n_cu = 0;                      // compute units (0: unknown)
     DevBuf plan_buf, hhi, hlo, ypart, logits, route_ids, route_w, hscratch;
     DevBuf gu_part;                    // shared expert's k-part gate/up sums (decode)
     int route_T = 0, route_E = 0;      // shape of the fp64 logits of the last router call
@@ -610,7 +611,7 @@ int moe_decode(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, 
     if (T == 1 && down_comb1_ok(layer->hidden, layer->inter, top_k, ctx->max_lds)) {
         // one token: down of every item and the combine in one launch
         Span sp(ctx, "down", s);
-        CX_HIP(launch_down_comb1(L, P.token_pairs, route_w, top_k, s));
+        CX_HIP(launch_down_comb1(L, P.token_pairs, route_w, top_k, ctx->n_cu, s));
         return CX_OK;
     }
     if (L.max_items > 0) {
@@ -957,6 +958,9 @@ int cx_ctx_create(int device, cx_ctx** out) {
     if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess &&
         lds > 0)
         c->max_lds = lds;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
+        c->n_cu = cus;
     (void)hipGetLastError();
     *out = c;
     return CX_OK;

@@ -225,6 +225,12 @@ int max_lds() {
     return v;
 }
 
+int n_cu() {
+    int v = 0;
+    KB_CHECK(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, 0));
+    return v;
+}
+
 // Bare stream of the one-token down's bytes (no compute): 9 matrices, the
 // k_down_item shape (workgroup = one item x 64 rows, full-K waves) or the
 // k_down_comb1 shape (workgroup = 16 rows x all items: wave w = item w's 16
@@ -298,6 +304,7 @@ int cmd_decode_down(int iters) {
     uint32_t* sink = nullptr;
     KB_CHECK(hipMalloc(&sink, 4096));
     const int lds = max_lds();
+    const int cus = n_cu();
     const double down_bytes = 9.0 * (kMat + 56 * 16 * 4) + 2.0 * kH;
     std::mt19937 rng(11);
     std::vector<DownPtrs> sets(16);
@@ -317,7 +324,7 @@ int cmd_decode_down(int iters) {
                    ExpertLaunch L = dp.launch(i, table, lds);
                    L.skip_shared = 0;
                    L.max_items = 9;
-                   KB_CHECK(launch_down_comb1(L, L.plan.token_pairs, dp.topk_w, 8, 0));
+                   KB_CHECK(launch_down_comb1(L, L.plan.token_pairs, dp.topk_w, 8, cus, 0));
                }), down_bytes);
         report("k_down_item (down, 9 items)", time_launches(iters, [&](int i) {
                    ExpertLaunch L = dp.launch(i, table, lds);
@@ -342,6 +349,7 @@ int cmd_placement(int iters) {
         DecodePlans dp(pool, 16, 3);
         cx_expert_desc* table = dev_copy(pool.d);
         const int lds = max_lds();
+        const int cus = n_cu();
         const double gu_bytes = 8.0 * (2 * kMat + 2 * 16 * 56 * 4) + kH * 2;
         const double down_bytes = 9.0 * (kMat + 56 * 16 * 4) + 2.0 * kH;
         report("k_gate_up_t (8 routed experts)", time_launches(iters, [&](int i) {
@@ -351,7 +359,7 @@ int cmd_placement(int iters) {
                    ExpertLaunch L = dp.launch(i, table, lds);
                    L.skip_shared = 0;
                    L.max_items = 9;
-                   KB_CHECK(launch_down_comb1(L, L.plan.token_pairs, dp.topk_w, 8, 0));
+                   KB_CHECK(launch_down_comb1(L, L.plan.token_pairs, dp.topk_w, 8, cus, 0));
                }), down_bytes);
         (void)hipFree(table);
     }

@@ -300,12 +300,16 @@ def test_moe_duplicate_route_is_dropped_and_reported(gpu, oracle, T, prefill):
     (1024, 1024, False, 4, torch.float16, torch.float16),
     (2048, 2048, True, 6, torch.bfloat16, torch.float16),
     (1024, 512, True, 1, torch.float16, torch.bfloat16),
-    (1024, 2048, False, 8, torch.bfloat16, torch.bfloat16)])
+    (1024, 2048, False, 8, torch.bfloat16, torch.bfloat16),
+    (1792, 2048, True, 8, torch.bfloat16, torch.bfloat16),
+    (1792, 1024, False, 7, torch.float16, torch.bfloat16)])
 def test_one_token_down_combine(gpu, oracle, H, I, shared, K, dtype, odtype):
     """One token (cx_moe_decode, routes given): the down projection of every
     item and the weighted combine run as one launch (k_down_comb1) for top_k
     <= 8 — inter of 4, 8 and 16 k-blocks, with and without a shared expert,
-    fewer routes than waves, mixed in/out dtypes."""
+    fewer routes than waves, mixed in/out dtypes.  Hidden 1792 on a 256-CU
+    device runs 14-row tiles (128 workgroups), some of which straddle two
+    128-row scale blocks; the 16-row cases keep whole tiles."""
     print(f"[moe] one-token down+combine H={H} I={I} shared={shared} K={K}", flush=True)
     E = 16
     layer, experts, sh, cpu, cpu_sh = _make_layer(gpu, oracle, E, H, I, seed=81 + K, shared=shared)
