@@ -11,6 +11,9 @@
 //                          in one launch) against k_down_item + k_combine_dec
 //   cx_kbench placement    one-token gate/up and down launches with the experts
 //                          packed into one buffer vs spread over 24 x 2 GiB chunks
+//   cx_kbench decode-balance  one-token gate/up bytes streamed bare with tiles
+//                          handed out statically or claimed from per-XCD counters,
+//                          and k_down_comb1 over 256 / 384 / 448 / 512 tiles
 //   cx_kbench grouped      the grouped prefill kernels on the config-3-like plan
 //
 // Bytes are synthetic (small finite fp8 codes, block scales 1e-3): the numbers
@@ -367,6 +370,136 @@ int cmd_placement(int iters) {
 }
 
 // ---------------------------------------------------------------------------
+// Tile balance at one token.  A tile of the routed gate/up = 16 rows x full K
+// of one expert's gate and up (4 waves x K/4, the k_gate_up_t shape), 8 x 128
+// tiles.  The bare stream (no compute) hands tiles out three ways — MODE 0:
+// workgroup b streams tiles b, b + grid, ...; MODE 1: per-XCD pools (tile
+// 8j + x for pool x = b % 8, the dispatcher's round-robin XCD), first tile
+// static, then claims from the pool's counter, requested before the current
+// tile streams and read after it.  Claims only grow, so every workgroup
+// exits and every tile is streamed once.
+struct GuPtrs {
+    const uint8_t* gate[8];
+    const uint8_t* up[8];
+};
+
+__device__ __forceinline__ uint32_t bare_gu_tile(const GuPtrs& P, int t) {
+    constexpr int NKB = 14, D = 4;
+    const int e = t >> 7, rt = t & 127;
+    const int wave = wave_id(), lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+    const size_t off = (size_t)(rt * 16 + c) * kH + (size_t)wave * NKB * kKB + g * 32;
+    const uint8_t* pg = P.gate[e] + off;
+    const uint8_t* pu = P.up[e] + off;
+    u32x4 wg[D][2], wu[D][2];
+    uint32_t acc = 0;
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+        wg[s][0] = ld16(pg + s * kKB);
+        wg[s][1] = ld16(pg + s * kKB + 16);
+        wu[s][0] = ld16(pu + s * kKB);
+        wu[s][1] = ld16(pu + s * kKB + 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < NKB; ++k) {
+        acc ^= fold(wg[k % D]) + fold(wu[k % D]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (k + D < NKB) {
+            wg[k % D][0] = ld16(pg + (k + D) * kKB);
+            wg[k % D][1] = ld16(pg + (k + D) * kKB + 16);
+            wu[k % D][0] = ld16(pu + (k + D) * kKB);
+            wu[k % D][1] = ld16(pu + (k + D) * kKB + 16);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return acc;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void k_bare_gu_tiles(GuPtrs P, uint32_t* sink, int* ctr) {
+    constexpr int n_tiles = 8 * 128, pool = n_tiles / 8;
+    __shared__ int next;
+    uint32_t acc = 0;
+    if (MODE == 0) {
+        for (int t = blockIdx.x; t < n_tiles; t += gridDim.x) acc ^= bare_gu_tile(P, t);
+    } else {
+        const int x = blockIdx.x & 7, per = gridDim.x >> 3;
+        int j = blockIdx.x >> 3;
+        while (j < pool) {
+            if (threadIdx.x == 0) next = atomicAdd(ctr + x * 32, 1) + per;
+            acc ^= bare_gu_tile(P, j * 8 + x);
+            __syncthreads();
+            j = next;
+            __syncthreads();
+        }
+    }
+    if (acc == 0x12345678u) sink[threadIdx.x] = acc;
+}
+
+int cmd_decode_balance(int iters) {
+    std::printf("decode-balance: one token, experts spread over 24 x 2 GiB\n");
+    Pool pool(true);
+    DecodePlans dp(pool, 16, 3);
+    cx_expert_desc* table = dev_copy(pool.d);
+    uint32_t* sink = nullptr;
+    int* ctr = nullptr;
+    KB_CHECK(hipMalloc(&sink, 4096));
+    KB_CHECK(hipMalloc(&ctr, 8 * 32 * sizeof(int)));
+    const int lds = max_lds();
+    const double gu_bytes = 8.0 * 2 * kMat;
+    std::mt19937 rng(13);
+    std::vector<GuPtrs> sets(16);
+    for (auto& s : sets)
+        for (int j = 0; j < 8; ++j) {
+            const cx_expert_desc& q = pool.d[rng() % pool.d.size()];
+            s.gate[j] = q.w_gate;
+            s.up[j] = q.w_up;
+        }
+    auto bare = [&](const char* what, int mode, int grid) {
+        report(what, time_launches(iters, [&](int i) {
+                   KB_CHECK(hipMemsetAsync(ctr, 0, 8 * 32 * sizeof(int), 0));
+                   if (mode == 0)
+                       cx_launch(k_bare_gu_tiles<0>, dim3(grid), dim3(256), 0u, (hipStream_t)0, sets[i % 16], sink, ctr);
+                   else
+                       cx_launch(k_bare_gu_tiles<1>, dim3(grid), dim3(256), 0u, (hipStream_t)0, sets[i % 16], sink, ctr);
+               }), gu_bytes);
+    };
+    // k_down_comb1 over the first `grid` tiles of `rows` rows (the library
+    // kernel; grids below hidden / rows leave the last rows unwritten)
+    const double tile_bytes = 9.0 * 16 * kI;
+    auto down = [&](const char* what, int grid, int rows) {
+        report(what, time_launches(iters, [&](int i) {
+                   ExpertLaunch L = dp.launch(i, table, lds);
+                   L.skip_shared = 0;
+                   L.max_items = 9;
+                   cx_launch((k_down_comb1<16, kDc1Depth>), dim3(grid), dim3(64 * kDc1Waves),
+                             (uint32_t)down_comb1_lds(kI), (hipStream_t)0, L, L.plan.token_pairs,
+                             (const float*)dp.topk_w, 8, rows);
+               }), tile_bytes / 16 * rows * grid);
+    };
+    for (int rep = 0; rep < 2; ++rep) {
+        std::printf(" pass %d\n", rep + 1);
+        report("k_gate_up_t (8 routed experts)", time_launches(iters, [&](int i) {
+                   KB_CHECK(launch_gate_up(dp.launch(i, table, lds), 0));
+               }), gu_bytes);
+        bare("bare gate/up: static, 1024 workgroups x 1 tile", 0, 1024);
+        bare("bare gate/up: static, 512 workgroups x 2 tiles", 0, 512);
+        bare("bare gate/up: static, 256 workgroups x 4 tiles", 0, 256);
+        bare("bare gate/up: per-XCD claims, 768 workgroups", 1, 768);
+        bare("bare gate/up: per-XCD claims, 512 workgroups", 1, 512);
+        bare("bare gate/up: per-XCD claims, 256 workgroups", 1, 256);
+        down("k_down_comb1: first 256 tiles of 16 rows", 256, 16);
+        down("k_down_comb1: first 384 tiles of 16 rows", 384, 16);
+        down("k_down_comb1: 448 tiles of 16 rows (all rows)", kH / 16, 16);
+        down("k_down_comb1: 512 tiles of 14 rows (all rows)", kH / 14, 14);
+    }
+    (void)hipFree(ctr);
+    (void)hipFree(sink);
+    (void)hipFree(table);
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
 // Config-3-like prefill plan: 512 tokens, 256 routed experts whose pair counts
 // follow 1 + 12 rank^-1.1 (sum 4096, max ~170), plus the shared expert's 512
 // pairs; items of <= 64 pairs as the general planner cuts them.
@@ -552,7 +685,8 @@ int main(int argc, char** argv) {
     if (!std::strcmp(cmd, "layout")) return cmd_layout(std::min(iters, 12));
     if (!std::strcmp(cmd, "decode-down")) return cmd_decode_down(iters);
     if (!std::strcmp(cmd, "placement")) return cmd_placement(iters);
+    if (!std::strcmp(cmd, "decode-balance")) return cmd_decode_balance(iters);
     if (!std::strcmp(cmd, "grouped")) return cmd_grouped(std::min(iters, 12));
-    std::fprintf(stderr, "usage: cx_kbench layout|decode-down|placement|grouped [launches]\n");
+    std::fprintf(stderr, "usage: cx_kbench layout|decode-down|placement|decode-balance|grouped [launches]\n");
     return 2;
 }
