@@ -474,12 +474,35 @@ def _sample_tokens(ids, T, n_hot=4, n_spread=4):
     return sorted(set(hot_tok + spread))
 
 
+def _decode_paths_agree(gpu, layer, x, ids, wts, yf_grouped):
+    """Every token of a grouped (prefill) call again through the decode
+    pipeline, which shares no GEMM kernel with it: alternate 16-token blocks
+    one token per call (routed gate/up + the one-launch down/combine) and 16
+    tokens per call (the B=16 kernels).  Both sum exact fp8 x activation
+    products in fp32, in different k orders, so they agree to rounding."""
+    T = x.shape[0]
+    outs = []
+    for t0 in range(0, T, 16):
+        t1 = min(T, t0 + 16)
+        if (t0 // 16) % 2 == 0:
+            for t in range(t0, t1):
+                outs.append(gpu.moe(layer, x[t:t + 1], ids[t:t + 1], wts[t:t + 1], want_f32=True)[1])
+        else:
+            outs.append(gpu.moe(layer, x[t0:t1], ids[t0:t1], wts[t0:t1], want_f32=True)[1])
+    gpu.sync()
+    dec = torch.cat(outs).cpu().numpy()
+    grp = yf_grouped.cpu().numpy()
+    assert rel_l2(dec, grp) < 1e-5, rel_l2(dec, grp)
+    assert np.abs(dec - grp).max() < 1e-2
+
+
 def test_config3_prefill_chunk_matches_oracle(gpu, oracle):
     """The config-3 benchmark call: 512 tokens through cx_moe_layer with a
     Zipf-skewed correction bias, 256 experts + shared at DeepSeek-V3 shapes
     (hot experts split into several 64-pair items).  Every token's routes
     against the oracle; the output of a token sample that includes the hottest
-    expert's tokens against the dequantise-then-fp32 oracle."""
+    expert's tokens against the dequantise-then-fp32 oracle; every token
+    against the decode pipeline."""
     print("[moe] config-3 prefill chunk", flush=True)
     E, H, T = 256, 7168, 512
     from constellation_amd.engine import Expert, Layer
@@ -506,6 +529,7 @@ def test_config3_prefill_chunk_matches_oracle(gpu, oracle):
         got = yf.cpu().numpy()[sample]
         assert rel_l2(got, ref) < 1e-5 and np.abs(got - ref).max() < 2e-2
         assert np.array_equal(_bits(y)[sample], oracle.encode_act(got, BF16, "rne"))
+        _decode_paths_agree(gpu, layer, x, ids, wts, yf)  # all 512 tokens
     finally:
         _free(layer, experts, sh)
 
@@ -514,7 +538,8 @@ def test_config4_node_share_layer_matches_oracle(gpu, oracle):
     """One layer of the config-4 node share: 64 resident experts of 256 (e = 0
     mod 4), no shared expert, 32 tokens routed under the resident mask with a
     Zipf-skewed bias (the grouped path).  Routes against the oracle's masked
-    router; a token sample against the oracle."""
+    router; a token sample against the oracle; every token against the
+    decode pipeline."""
     print("[moe] config-4 node-share layer", flush=True)
     E, H, T = 256, 7168, 32
     from constellation_amd.engine import Expert, Layer
@@ -540,6 +565,7 @@ def test_config4_node_share_layer_matches_oracle(gpu, oracle):
                           x.float().cpu().numpy()[sample], idn[sample], wn[sample])
         got = yf.cpu().numpy()[sample]
         assert rel_l2(got, ref) < 1e-5 and np.abs(got - ref).max() < 2e-2
+        _decode_paths_agree(gpu, layer, x, ids, wts, yf)  # all 32 tokens
     finally:
         torch.cuda.synchronize()
         layer.close()
