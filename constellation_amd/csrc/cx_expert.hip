@@ -31,6 +31,7 @@
 #include "cx_down.h"
 #include "cx_gate_up.h"
 #include "cx_grouped.h"
+#include "cx_big.h"
 
 namespace cx {
 namespace {
@@ -918,6 +919,71 @@ hipError_t launch_down(const ExpertLaunch& L, hipStream_t s) {
     if (!done) {
         if (L.maxt == 1) cx_launch((k_down_rt<1>), grid, dim3(256), 0, s, L);
         else cx_launch((k_down_rt<4>), grid, dim3(256), 0, s, L);
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Grouped GEMM for items of up to 128 pairs (cx_big.h).  Each ring stage is
+// its own LDS array (static, one workgroup per CU), so the compiler's waits
+// for the stage DMA do not cover the stages still in flight.
+namespace {
+
+template <int NKB, bool F16>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k_gu_big(ExpertLaunch L) {
+    __shared__ __attribute__((aligned(16))) unsigned char s0[kBigGuA + kBigGuB];
+    __shared__ __attribute__((aligned(16))) unsigned char s1[kBigGuA + kBigGuB];
+    __shared__ __attribute__((aligned(16))) unsigned char s2[kBigGuA + kBigGuB];
+    __shared__ __attribute__((aligned(16))) unsigned char s3[kBigGuA + kBigGuB];
+    unsigned char* const st[kBigGuRing] = {s0, s1, s2, s3};
+    big_gate_up<NKB, F16>(L, st);
+}
+
+template <int NKB>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k_dn_big(ExpertLaunch L) {
+    __shared__ __attribute__((aligned(16))) unsigned char s0[kBigDnA + 2 * kBigDnB];
+    __shared__ __attribute__((aligned(16))) unsigned char s1[kBigDnA + 2 * kBigDnB];
+    __shared__ __attribute__((aligned(16))) unsigned char s2[kBigDnA + 2 * kBigDnB];
+    unsigned char* const st[kBigDnRing] = {s0, s1, s2};
+    big_down<NKB>(L, st);
+}
+
+// grid: every (item, row tile) of the plan's bound, rounded up to whole XCD
+// rows (big_tile maps the tiles that exist)
+dim3 big_grid(int items, int row_tiles) { return dim3((items * row_tiles + 7) / 8 * 8); }
+
+}  // namespace
+
+bool big_shape_ok(int hidden, int inter, int in_dtype) {
+    if (inter % kBigGuRows != 0 || hidden % kBigDnRows != 0) return false;
+    const int nkg = hidden / kKB, nkd = inter / kKB;
+    return (nkg == 56 || nkg == 16 || nkg == 8) && (nkd == 16 || nkd == 8 || nkd == 4) &&
+           (in_dtype == CX_DTYPE_BF16 || in_dtype == CX_DTYPE_FP16);
+}
+
+bool big_ok(const ExpertLaunch& L) {
+    return L.table != nullptr && big_shape_ok(L.hidden, L.inter, L.in_dtype);
+}
+
+hipError_t launch_gate_up_big(const ExpertLaunch& L, hipStream_t s) {
+    if (!big_ok(L)) return hipErrorInvalidValue;
+    const dim3 grid = big_grid(L.max_items, L.inter / kBigGuRows), block(512);
+    const bool f16 = L.in_dtype == CX_DTYPE_FP16;
+    switch (L.hidden / kKB) {
+        case 56: f16 ? cx_launch((k_gu_big<56, true>), grid, block, 0, s, L) : cx_launch((k_gu_big<56, false>), grid, block, 0, s, L); break;
+        case 16: f16 ? cx_launch((k_gu_big<16, true>), grid, block, 0, s, L) : cx_launch((k_gu_big<16, false>), grid, block, 0, s, L); break;
+        default: f16 ? cx_launch((k_gu_big<8, true>), grid, block, 0, s, L) : cx_launch((k_gu_big<8, false>), grid, block, 0, s, L); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_down_big(const ExpertLaunch& L, hipStream_t s) {
+    if (!big_ok(L)) return hipErrorInvalidValue;
+    const dim3 grid = big_grid(L.max_items, L.hidden / kBigDnRows), block(512);
+    switch (L.inter / kKB) {
+        case 16: cx_launch((k_dn_big<16>), grid, block, 0, s, L); break;
+        case 8: cx_launch((k_dn_big<8>), grid, block, 0, s, L); break;
+        default: cx_launch((k_dn_big<4>), grid, block, 0, s, L); break;
     }
     return hipGetLastError();
 }

@@ -24,6 +24,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kKB = 128;        // k-block: one scale per 128 columns
 constexpr int kTileRows = 16;   // MFMA 16x16x32: 16 weight rows per wave
 constexpr int kTileTok = 16;    // 16 token (pair) columns per MFMA tile
+constexpr int kBigPairs = 128;  // pairs per item of the LDS-ring grouped GEMM (many tokens per expert)
 constexpr int kWaves = 4;       // waves per workgroup
 
 // ---------------------------------------------------------------------------
@@ -148,6 +149,13 @@ struct ExpertLaunch {
 };
 
 hipError_t launch_gate_up(const ExpertLaunch& L, hipStream_t s);
+// Grouped mode with items of up to kBigPairs (128) pairs, for calls with
+// many tokens per expert (cx_big.h): gate/up writes h, down writes y_part,
+// as launch_gate_up / launch_down do.  big_ok: the shapes they take.
+bool big_shape_ok(int hidden, int inter, int in_dtype);
+bool big_ok(const ExpertLaunch& L);
+hipError_t launch_gate_up_big(const ExpertLaunch& L, hipStream_t s);
+hipError_t launch_down_big(const ExpertLaunch& L, hipStream_t s);
 // Down projection per work item: grouped mode writes fp32 y_part[pair]
 // (combined afterwards by launch_combine), single mode writes y / y_f32.
 hipError_t launch_down(const ExpertLaunch& L, hipStream_t s);

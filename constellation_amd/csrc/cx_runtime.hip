@@ -645,6 +645,15 @@ int moe_run(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int
     const bool dec = !prefill && n_tokens <= kTileTok && dec_path_ok(layer, top_k, route);
     PlanSizes z = plan_sizes(n_tokens, top_k, layer->n_experts, layer->has_shared);
     if (dec) z.max_items = z.max_slots;  // one item per slot (<= 16 pairs each)
+    // Calls with at least kBigPairs pairs per routed expert on average: the
+    // experts' weights serve hundreds of columns, so 128-pair items through
+    // the LDS-ring GEMM instead of 64-pair items that each re-stream them.
+    const bool big = !dec && big_shape_ok(layer->hidden, layer->inter, in_dtype) &&
+                     (int64_t)n_tokens * top_k >= (int64_t)kBigPairs * layer->n_experts;
+    if (big) {
+        z.item_cap = kBigPairs;
+        z.max_items = z.max_slots + (z.max_pairs + kBigPairs - 1) / kBigPairs;
+    }
     if (z.max_pairs == 0) return fail(CX_EINVAL, "nothing to compute");
     PlanPtrs P;
     if ((rc = carve_plan(ctx, z, n_tokens, top_k, dec, s, &P))) return rc;
@@ -689,11 +698,11 @@ int moe_run(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int
     L.max_lds = ctx->max_lds;
     {
         Span sp(ctx, "gate_up", s);
-        CX_HIP(launch_gate_up(L, s));
+        CX_HIP(big ? launch_gate_up_big(L, s) : launch_gate_up(L, s));
     }
     {
         Span sp(ctx, "down", s);
-        CX_HIP(launch_down(L, s));
+        CX_HIP(big ? launch_down_big(L, s) : launch_down(L, s));
     }
     {
         Span sp(ctx, "combine", s);

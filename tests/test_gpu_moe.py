@@ -159,6 +159,70 @@ def test_moe_grouped_vs_oracle(gpu, oracle, T, prefill, I):
         _free(layer, experts, sh)
 
 
+@pytest.mark.parametrize("H,I,E,T,K,dtype,shared", [
+    (1024, 512, 5, 160, 4, torch.bfloat16, True),
+    (2048, 1024, 4, 136, 4, torch.float16, False),
+    (1024, 2048, 6, 200, 4, torch.bfloat16, True)])
+def test_moe_many_tokens_per_expert(gpu, oracle, H, I, E, T, K, dtype, shared):
+    """Calls with >= 128 pairs per routed expert on average take 128-pair
+    items through the LDS-ring GEMM: experts cut into a full item plus a
+    partial one, or a single partial item; hidden of 8 and 16 k-blocks,
+    inter of 4, 8 and 16; bf16 and fp16 activations.  Every token against
+    the oracle."""
+    print(f"[moe] many tokens per expert H={H} I={I} E={E} T={T}", flush=True)
+    assert T * K >= 128 * E
+    layer, experts, sh, cpu, cpu_sh = _make_layer(gpu, oracle, E, H, I, seed=61 + E, shared=shared)
+    try:
+        x = gpu.gen_normal(62 + E, 1, (T, H), 1.0, dtype)
+        rng = np.random.default_rng(E)
+        ids = np.stack([rng.choice(E, K, replace=False) for _ in range(T)]).astype(np.int32)
+        wts = rng.uniform(0.05, 1.0, ids.shape).astype(np.float32)
+        y, yf = gpu.moe(layer, x, torch.from_numpy(ids).cuda(), torch.from_numpy(wts).cuda(),
+                        want_f32=True, prefill=True)
+        gpu.sync()
+        ref = _oracle_moe(oracle, cpu, cpu_sh, x.float().cpu().numpy(), ids, wts)
+        yf = yf.cpu().numpy()
+        assert rel_l2(yf, ref) < 1e-5, rel_l2(yf, ref)
+        assert np.abs(yf - ref).max() < 2e-2
+        code = BF16 if dtype == torch.bfloat16 else FP16
+        assert np.array_equal(_bits(y), oracle.encode_act(yf, code, "rne"))
+    finally:
+        _free(layer, experts, sh)
+
+
+def test_full_size_many_tokens_per_expert(gpu, oracle):
+    """DeepSeek-V3 shapes (H=7168, I=2048) through the LDS-ring GEMM: 8
+    routed experts + shared, 256 tokens x 4 routes (128 pairs per expert on
+    average).  A token sample against the oracle, every token against the
+    decode pipeline."""
+    print("[moe] full-size many tokens per expert", flush=True)
+    E, H, T, K = 8, 7168, 256, 4
+    from constellation_amd.engine import Expert, Layer
+    experts = [Expert.generate(0, 71, 0x5000 + 4 * e) for e in range(E)]
+    sh = Expert.generate(0, 71, 0x5000 + 4 * E)
+    layer = Layer(gpu, experts, sh)
+    try:
+        x = gpu.gen_normal(72, 1, (T, H), 1.0, torch.bfloat16)
+        rng = np.random.default_rng(73)
+        ids = np.stack([rng.choice(E, K, replace=False) for _ in range(T)]).astype(np.int32)
+        wts = rng.uniform(0.05, 1.0, ids.shape).astype(np.float32)
+        ids_d, wts_d = torch.from_numpy(ids).cuda(), torch.from_numpy(wts).cuda()
+        y, yf = gpu.moe(layer, x, ids_d, wts_d, want_f32=True, prefill=True)
+        gpu.sync()
+        sel = np.array([0, 1, 77, 128, 200, 255])
+        cpu = {e: oracle.gen_expert(71, 0x5000 + 4 * e) for e in sorted(set(ids[sel].ravel().tolist()))}
+        cpu_sh = oracle.gen_expert(71, 0x5000 + 4 * E)
+        ref = _oracle_moe(oracle, [cpu.get(e) for e in range(E)], cpu_sh,
+                          x.float().cpu().numpy()[sel], ids[sel], wts[sel])
+        got = yf.cpu().numpy()[sel]
+        assert rel_l2(got, ref) < 1e-5, rel_l2(got, ref)
+        assert np.abs(got - ref).max() < 2e-2
+        assert np.array_equal(_bits(y)[sel], oracle.encode_act(got, BF16, "rne"))
+        _decode_paths_agree(gpu, layer, x, ids_d, wts_d, yf)
+    finally:
+        _free(layer, experts, sh)
+
+
 def test_moe_prefill_hot_expert_splits_items(gpu, oracle):
     """One expert routed by every token (> 64 pairs -> several work items)."""
     print("[moe] hot expert", flush=True)
