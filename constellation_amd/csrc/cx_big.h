@@ -120,9 +120,12 @@ __device__ __forceinline__ void big_ring(Issue& issue, Compute& compute) {
     }
 }
 
-// LDS row layouts (16-byte chunks XOR-swizzled by row):
+// LDS row layouts (16-byte chunks XOR-swizzled by row; both keys measured
+// free of bank conflicts for these fragment reads with SQ_LDS_BANK_CONFLICT,
+// where plain rows cost 4-12 conflict cycles per ds_read_b128):
 //  * weight rows of 64 B: chunk q of row r at chunk q ^ ((r >> 1) & 3);
-//  * activation rows of 128 B (64 values): chunk q of row t at q ^ (t & 7).
+//  * activation rows of 128 B (64 values): chunk q of row t at
+//    q ^ (t & 7) ^ ((t >> 3) & 1).
 // MFMA step j (0, 1) of a stage covers, in lane group g = lane / 16, the 8
 // k values 16 g + 8 j ..: weight chunk g holds both steps' bytes, activation
 // chunks 2 g + j.
@@ -163,7 +166,7 @@ __device__ __forceinline__ void big_gate_up(const ExpertLaunch& L, unsigned char
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
         const int tp = 8 * (2 * wave + m) + (lane >> 3);
-        const int q = (lane & 7) ^ (tp & 7);
+        const int q = (lane & 7) ^ (tp & 7) ^ ((tp >> 3) & 1);
         const int tok = ldi(L.plan.pair_token + u.pb + min(tp, u.np - 1));
         bsrc[m] = static_cast<const uint16_t*>(L.x) + (size_t)tok * H + 8 * q;
     }
@@ -189,7 +192,7 @@ __device__ __forceinline__ void big_gate_up(const ExpertLaunch& L, unsigned char
     const int aoff = c * kBigK + 16 * (g ^ ((c >> 1) & 3));
     int boff[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) boff[j] = c * 128 + 16 * ((2 * g + j) ^ (c & 7));
+    for (int j = 0; j < 2; ++j) boff[j] = c * 128 + 16 * ((2 * g + j) ^ (c & 7) ^ ((c >> 3) & 1));
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
     f32x4 acc[2][2][4], part[2][2][4];  // [gate/up][row tile][pair tile]
 #pragma unroll
@@ -311,7 +314,7 @@ __device__ __forceinline__ void big_down(const ExpertLaunch& L, unsigned char* c
     for (int m = 0; m < 4; ++m) {
         const int i = 4 * wave + m;
         const int tp = 8 * (i & 15) + (lane >> 3);
-        const int q = (lane & 7) ^ (tp & 7);
+        const int q = (lane & 7) ^ (tp & 7) ^ ((tp >> 3) & 1);
         bsrc[m] = ((i >> 4) ? L.h_lo : L.h_hi) + (size_t)(u.pb + min(tp, u.np - 1)) * I + 8 * q;
     }
     float scd[4];
@@ -332,7 +335,7 @@ __device__ __forceinline__ void big_down(const ExpertLaunch& L, unsigned char* c
     const int aoff = c * kBigK + 16 * (g ^ ((c >> 1) & 3));
     int boff[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) boff[j] = c * 128 + 16 * ((2 * g + j) ^ (c & 7));
+    for (int j = 0; j < 2; ++j) boff[j] = c * 128 + 16 * ((2 * g + j) ^ (c & 7) ^ ((c >> 3) & 1));
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
     f32x4 acc[4][4], part[4][4];  // [row tile][pair tile]
 #pragma unroll
