@@ -73,6 +73,10 @@ __device__ __forceinline__ void big_lds_read4(uint32_t base, u32x4 (&v)[4]) {
     v[2] = big_lds_read<OFF + 2 * STRIDE>(base);
     v[3] = big_lds_read<OFF + 3 * STRIDE>(base);
 }
+__device__ __forceinline__ void big_lds_wait(u32x4 (&a)[4], u32x4 (&b)[4]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
+}
 template <int N>
 __device__ __forceinline__ void big_lds_wait(u32x4 (&v)[N]) {
     static_assert(N == 4 || N == 8, "fragment batch");
@@ -211,18 +215,18 @@ __device__ __forceinline__ void big_gate_up(const ExpertLaunch& L, unsigned char
         aw[1] = big_lds_read<16 * kBigK>(ab);
         aw[2] = big_lds_read<kBigGuRows * kBigK>(ab);
         aw[3] = big_lds_read<(kBigGuRows + 16) * kBigK>(ab);
-        big_lds_wait(aw);
-        // one MFMA step at a time (fragments of both steps live at once
-        // would not fit beside the accumulators and partial sums)
+        u32x4 br[2][4];  // [step][pair tile]: pairs wp * 64 + tt * 16
+        big_lds_read4<0, 16 * 128>(sb + kBigGuA + wp * 64 * 128 + boff[0], br[0]);
+        big_lds_wait(aw, br[0]);
+        // the second step's x fragments load under the first step's MFMAs
+        big_lds_read4<0, 16 * 128>(sb + kBigGuA + wp * 64 * 128 + boff[1], br[1]);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             __builtin_amdgcn_sched_barrier(0);
-            u32x4 br[4];  // pairs wp * 64 + tt * 16
-            big_lds_read4<0, 16 * 128>(sb + kBigGuA + wp * 64 * 128 + boff[j], br);
-            big_lds_wait(br);
+            if (j == 1) big_lds_wait(br[1]);
             V bx[4];
 #pragma unroll
-            for (int tt = 0; tt < 4; ++tt) bx[tt] = M::bits(br[tt]);
+            for (int tt = 0; tt < 4; ++tt) bx[tt] = M::bits(br[j][tt]);
 #pragma unroll
             for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -346,29 +350,33 @@ __device__ __forceinline__ void big_down(const ExpertLaunch& L, unsigned char* c
         const uint32_t sb = big_lds_addr(st[slot]);
         u32x4 aw[4];  // rows wr * 64 + rt * 16
         big_lds_read4<0, 16 * kBigK>(sb + wr * 64 * kBigK + aoff, aw);
-        big_lds_wait(aw);
+        // four batches of x fragments: (step j, plane pl) = (0,hi) (0,lo)
+        // (1,hi) (1,lo), each loading under the previous batch's MFMAs
+        const uint32_t bb[2] = {sb + kBigDnA + wp * 64 * 128 + boff[0], sb + kBigDnA + wp * 64 * 128 + boff[1]};
+        u32x4 br[2][4];
+        big_lds_read4<0, 16 * 128>(bb[0], br[0]);
+        big_lds_wait(aw, br[0]);
+        V a[4];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int bt = 0; bt < 4; ++bt) {
+            const int j = bt >> 1;
             __builtin_amdgcn_sched_barrier(0);
-            V a[4];
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt) a[rt] = M::cvt(aw[rt][2 * j], aw[rt][2 * j + 1]);
-            // hi plane, then lo, against the same converted weights
-#pragma unroll
-            for (int pl = 0; pl < 2; ++pl) {
-                __builtin_amdgcn_sched_barrier(0);
-                u32x4 br[4];  // pairs wp * 64 + tt * 16 of plane pl
-                const uint32_t bb = sb + kBigDnA + wp * 64 * 128 + boff[j];
-                if (pl == 0) big_lds_read4<0, 16 * 128>(bb, br);
-                else big_lds_read4<kBigDnB, 16 * 128>(bb, br);
-                big_lds_wait(br);
-#pragma unroll
-                for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-                    for (int tt = 0; tt < 4; ++tt)
-                        part[rt][tt] = M::mma(a[rt], M::bits(br[tt]),
-                                              (h == 0 && j == 0 && pl == 0) ? zero : part[rt][tt]);
+            if (bt + 1 < 4) {
+                const int jn = (bt + 1) >> 1;
+                if (((bt + 1) & 1) == 0) big_lds_read4<0, 16 * 128>(bb[jn], br[(bt + 1) & 1]);
+                else big_lds_read4<kBigDnB, 16 * 128>(bb[jn], br[(bt + 1) & 1]);
             }
+            if ((bt & 1) == 0) {
+#pragma unroll
+                for (int rt = 0; rt < 4; ++rt) a[rt] = M::cvt(aw[rt][2 * j], aw[rt][2 * j + 1]);
+            }
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt)
+                    part[rt][tt] = M::mma(a[rt], M::bits(br[bt & 1][tt]), (h == 0 && bt == 0) ? zero : part[rt][tt]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (bt + 1 < 4) big_lds_wait(br[(bt + 1) & 1]);
         }
         if (h == 1) {
             const int kb = s >> 1;
