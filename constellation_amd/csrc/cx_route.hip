@@ -23,6 +23,7 @@
 //    shared expert's gate/up (29 MB of weights) streams from HBM on the
 //    otherwise idle CUs meanwhile (its down projection joins the routed
 //    experts' down launch).
+#include <atomic>
 #include <algorithm>
 
 #include "cx_down.h"
@@ -809,13 +810,17 @@ constexpr int kPlanThreads = 1024;
 
 // Staged planner: the same plan as plan_build with every input first copied
 // into LDS in one round of independent loads (routes, layer table), so the
-// passes that follow wait only on LDS and the block barriers.  LDS layout:
-// table[E+1] | ids[n] | ok[n] | cnt[E] | cur[E] | scan[nt] | slot arrays
-// (expert, first pair, count) [E+1] each.
+// passes that follow wait only on LDS and the block barriers.  Routes are
+// held as 16-bit expert ids (clamped to [-1, E]; a route found invalid is
+// set to -1 once every thread has checked its token's repeats), each
+// thread keeping its routes' validity in a 64-bit mask: up to 64 routes per
+// thread.  LDS layout: table[E+1] | ids16[n, even] | cnt[E] | cur[E] |
+// scan[nt] | slot arrays (expert, first pair, count) [E+1] each.
+constexpr int kPlanRoutesPerThread = 64;
+
 size_t plan_staged_lds(int n_assign, int n_experts, int threads) {
-    return sizeof(cx_expert_desc) * ((size_t)n_experts + 1) +
-           sizeof(int) * (2 * (size_t)n_assign + 2 * (size_t)n_experts + threads +
-                          3 * ((size_t)n_experts + 1));
+    return sizeof(cx_expert_desc) * ((size_t)n_experts + 1) + 2 * (((size_t)n_assign + 1) & ~(size_t)1) +
+           sizeof(int) * (2 * (size_t)n_experts + threads + 3 * ((size_t)n_experts + 1));
 }
 
 __device__ __forceinline__ void plan_build_staged(const int32_t* __restrict__ ids,
@@ -828,9 +833,8 @@ __device__ __forceinline__ void plan_build_staged(const int32_t* __restrict__ id
     const int E = n_experts, n_assign = n_tokens * top_k;
     const int tid = threadIdx.x, nt = blockDim.x;
     cx_expert_desc* tab = reinterpret_cast<cx_expert_desc*>(lds);
-    int* sid = reinterpret_cast<int*>(tab + E + 1);
-    int* okv = sid + n_assign;
-    int* cnt = okv + n_assign;
+    int16_t* sid = reinterpret_cast<int16_t*>(tab + E + 1);
+    int* cnt = reinterpret_cast<int*>(sid + ((n_assign + 1) & ~1));
     int* cur = cnt + E;
     int* scan = cur + E;
     int* s_exp = scan + nt;
@@ -842,15 +846,16 @@ __device__ __forceinline__ void plan_build_staged(const int32_t* __restrict__ id
         const u32x4* src = reinterpret_cast<const u32x4*>(table);
         u32x4* dst = reinterpret_cast<u32x4*>(tab);
         for (int i = tid; i < (E + 1) * kChunks; i += nt) dst[i] = ld16(src + i);
-        for (int i = tid; i < n_assign; i += nt) sid[i] = ldi(ids + i);
+        for (int i = tid; i < n_assign; i += nt) sid[i] = (int16_t)max(-1, min(ldi(ids + i), E));
         for (int e = tid; e < E; e += nt) cnt[e] = 0;
         if (tid == 0) s_err = 0;
     }
     __syncthreads();
-    // 2) validity (range, residency, repeats within the token) and counts
-    for (int i = tid; i < n_assign; i += nt) {
+    // 2) validity (range, residency, repeats within the token) and counts;
+    // then invalid routes -> -1
+    uint64_t okm = 0;
+    for (int i = tid, r = 0; i < n_assign; i += nt, ++r) {
         const int e = sid[i];
-        int ok = 0;
         if (e >= 0) {
             if (e >= E) atomicOr(&s_err, kErrBadExpertId);
             else if (tab[e].w_up == nullptr) atomicOr(&s_err, kErrNotResident);
@@ -859,13 +864,15 @@ __device__ __forceinline__ void plan_build_staged(const int32_t* __restrict__ id
                 for (int j = (i / top_k) * top_k; j < i; ++j) dup |= sid[j] == e;
                 if (dup) atomicOr(&s_err, kErrDuplicateRoute);
                 else {
-                    ok = 1;
+                    okm |= 1ull << r;
                     atomicAdd(&cnt[e], 1);
                 }
             }
         }
-        okv[i] = ok;
     }
+    __syncthreads();
+    for (int i = tid, r = 0; i < n_assign; i += nt, ++r)
+        if (!((okm >> r) & 1)) sid[i] = -1;
     __syncthreads();
     // 3) slots in ascending expert id (block scans over per-thread ranges)
     const bool shared = has_shared && tab[E].w_up != nullptr;
@@ -900,7 +907,7 @@ __device__ __forceinline__ void plan_build_staged(const int32_t* __restrict__ id
     for (int i = tid; i < n_assign; i += nt) {
         const int t = i / top_k, k = i - t * top_k;
         int pos = -1;
-        if (okv[i]) {
+        if (sid[i] >= 0) {
             pos = atomicAdd(&cur[sid[i]], 1);
             P.pair_token[pos] = t;
             P.pair_weight[pos] = w[i];
@@ -1660,12 +1667,32 @@ hipError_t launch_route(const RouteArgs& R, hipStream_t s) {
                        R.item_cap, R.max_items, *R.plan, R.err_flag, s);
 }
 
+// Dynamic LDS the current device grants one workgroup (queried once per device).
+int plan_lds_limit() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        (void)hipGetLastError();
+        return 65536;
+    }
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0) {
+            (void)hipGetLastError();
+            v = 65536;
+        }
+        cache[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
 hipError_t launch_plan(const int32_t* ids, const float* w, int n_tokens, int top_k,
                        const cx_expert_desc* table, int n_experts, int has_shared, int item_cap,
                        int max_items, PlanPtrs plan, int* err_flag, hipStream_t s) {
     const int threads = n_tokens * top_k <= 512 ? 256 : kPlanThreads;
     const size_t staged = plan_staged_lds(n_tokens * top_k, n_experts, threads);
-    if (staged <= 65536) {
+    if (n_experts < 32768 && n_tokens * top_k <= kPlanRoutesPerThread * threads &&
+        staged <= (size_t)plan_lds_limit()) {
         cx_launch(k_plan_staged, dim3(1), dim3(threads), staged, s, ids, w, n_tokens, top_k,
                   table, n_experts, has_shared, item_cap, max_items, plan, err_flag);
         return hipGetLastError();

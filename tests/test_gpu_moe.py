@@ -190,6 +190,57 @@ def test_moe_many_tokens_per_expert(gpu, oracle, H, I, E, T, K, dtype, shared):
         _free(layer, experts, sh)
 
 
+def test_planner_many_routes_vs_oracle(gpu, oracle):
+    """4800 routes (1200 tokens x 4): more than the planner held in LDS as
+    32-bit ids; staged as 16-bit ids with the validity bits in registers.
+    Every token against the oracle (shared expert on, the LDS-ring GEMM)."""
+    print("[moe] planner 4800 routes", flush=True)
+    E, H, I, T, K = 8, 1024, 512, 1200, 4
+    layer, experts, sh, cpu, cpu_sh = _make_layer(gpu, oracle, E, H, I, seed=64, shared=True)
+    try:
+        x = gpu.gen_normal(65, 1, (T, H), 1.0, torch.bfloat16)
+        rng = np.random.default_rng(66)
+        ids = np.stack([rng.choice(E, K, replace=False) for _ in range(T)]).astype(np.int32)
+        wts = rng.uniform(0.05, 1.0, ids.shape).astype(np.float32)
+        y, yf = gpu.moe(layer, x, torch.from_numpy(ids).cuda(), torch.from_numpy(wts).cuda(),
+                        want_f32=True, prefill=True)
+        gpu.sync()
+        ref = _oracle_moe(oracle, cpu, cpu_sh, x.float().cpu().numpy(), ids, wts)
+        yf = yf.cpu().numpy()
+        assert rel_l2(yf, ref) < 1e-5, rel_l2(yf, ref)
+        assert np.abs(yf - ref).max() < 2e-2
+        assert np.array_equal(_bits(y), oracle.encode_act(yf, BF16, "rne"))
+    finally:
+        _free(layer, experts, sh)
+
+
+def test_planner_beyond_staging_matches_chunks(gpu, oracle):
+    """68,000 routes (17,000 tokens x 4) exceed what the staged planner holds
+    (64 per thread) and take the general planner; the same routes in four
+    chunks take the staged one.  A pair's value does not depend on its item's
+    other pairs, so the outputs are bit-identical."""
+    print("[moe] planner beyond staging", flush=True)
+    E, H, I, T, K = 4, 1024, 512, 17000, 4
+    layer, experts, sh, cpu, cpu_sh = _make_layer(gpu, oracle, E, H, I, seed=67, shared=False)
+    try:
+        x = gpu.gen_normal(68, 1, (T, H), 1.0, torch.bfloat16)
+        rng = np.random.default_rng(69)
+        ids = torch.from_numpy(np.stack([rng.permutation(E) for _ in range(T)]).astype(np.int32)).cuda()
+        wts = torch.from_numpy(rng.uniform(0.05, 1.0, (T, K)).astype(np.float32)).cuda()
+        y_all, yf_all = gpu.moe(layer, x, ids, wts, want_f32=True, prefill=True)
+        parts = [gpu.moe(layer, x[c:c + 4250], ids[c:c + 4250], wts[c:c + 4250], want_f32=True, prefill=True)[1]
+                 for c in range(0, T, 4250)]
+        gpu.sync()
+        assert torch.equal(yf_all, torch.cat(parts))
+        sel = np.array([0, 4249, 4250, 9000, 16999])
+        ref = _oracle_moe(oracle, cpu, None, x.float().cpu().numpy()[sel], ids.cpu().numpy()[sel],
+                          wts.cpu().numpy()[sel])
+        got = yf_all.cpu().numpy()[sel]
+        assert rel_l2(got, ref) < 1e-5 and np.abs(got - ref).max() < 2e-2
+    finally:
+        _free(layer, experts, sh)
+
+
 def test_full_size_many_tokens_per_expert(gpu, oracle):
     """DeepSeek-V3 shapes (H=7168, I=2048) through the LDS-ring GEMM: 8
     routed experts + shared, 256 tokens x 4 routes (128 pairs per expert on
