@@ -193,6 +193,29 @@ def _x4(gpu, stream, dt):
 
 
 @pytest.mark.parametrize("in_dt", [BF16, FP16])
+def test_single_expert_one_tile_item_full_size(gpu, oracle, in_dt):
+    """70 tokens of one full-size expert: a 64-token item and a 6-token one,
+    whose gate/up stages x in LDS chunks (one-tile items).  Every row against
+    the oracle."""
+    print(f"[expert] full size T=70 in={in_dt}", flush=True)
+    e = _full_expert(13, 0x720)
+    try:
+        x = gpu.gen_normal(14, 0x730, (70, 7168), 1.0, torch.bfloat16)
+        if in_dt == FP16:
+            x = x.to(torch.float16)
+        y, yf = gpu.expert_run(e, x, want_f32=True)
+        gpu.sync()
+        cpu = oracle.gen_expert(13, 0x720)
+        _, yref = oracle.expert_ref(cpu, oracle.decode_act(_bits(x), in_dt))
+        yf = yf.cpu().numpy()
+        assert rel_l2(yf, yref) < 1e-5, rel_l2(yf, yref)
+        assert np.abs(yf - yref).max() <= 2e-2
+        assert np.array_equal(_bits(y), oracle.encode_act(yf, in_dt, "rne"))
+    finally:
+        e.free()
+
+
+@pytest.mark.parametrize("in_dt", [BF16, FP16])
 def test_small_batch_expert_full_size(gpu, oracle, in_dt):
     """1..4 tokens take the k-part gate/up + split-K down launches (activations
     staged in LDS up to 3 tokens, through the weight ring at 4); 5 tokens the
