@@ -49,6 +49,20 @@ __device__ __forceinline__ int big_tile(int n) {
     return ((b >> 3) < per && t < n) ? t : -1;
 }
 
+// Logical tile -> (item, row tile): groups of kBigGroup consecutive items
+// (an expert's items are consecutive in the plan) walk their row tiles
+// together, so the workgroups that share a row tile's weights run side by
+// side on one XCD and its L2 serves them one fetch.  false past the items.
+constexpr int kBigGroup = 4;
+__device__ __forceinline__ bool big_item_tile(int t, int n_items, int n_rt, int* item, int* tile) {
+    const int span = kBigGroup * n_rt;
+    const int g = t / span, r = t - g * span;
+    const int in_group = min(kBigGroup, n_items - g * kBigGroup);
+    *tile = r / in_group;
+    *item = g * kBigGroup + (r - *tile * in_group);
+    return *tile < n_rt;
+}
+
 // Fragment reads from the LDS ring.  As plain loads the compiler cannot tell
 // which stage a pending global->LDS DMA writes and waits for all of them
 // (vmcnt(0)) before reading any stage, draining the ring; as asm it inserts
@@ -147,7 +161,8 @@ __device__ __forceinline__ void big_gate_up(const ExpertLaunch& L, unsigned char
     const int n_rt = L.inter / kBigGuRows;
     const int t = big_tile(n_items * n_rt);
     if (t < 0) return;
-    const int item = t / n_rt, tile = t - item * n_rt;
+    int item, tile;
+    if (!big_item_tile(t, n_items, n_rt, &item, &tile)) return;
     Unit u;
     if (!resolve_unit<false>(L, item, kBigPairs, &u)) return;
     const int H = u.e.hidden, I = u.e.inter;
@@ -297,7 +312,8 @@ __device__ __forceinline__ void big_down(const ExpertLaunch& L, unsigned char* c
     const int n_rt = L.hidden / kBigDnRows;
     const int t = big_tile(n_items * n_rt);
     if (t < 0) return;
-    const int item = t / n_rt, tile = t - item * n_rt;
+    int item, tile;
+    if (!big_item_tile(t, n_items, n_rt, &item, &tile)) return;
     Unit u;
     if (!resolve_unit<false>(L, item, kBigPairs, &u)) return;
     const int H = u.e.hidden, I = u.e.inter;
