@@ -259,6 +259,7 @@ struct cx_layer {
     cx_expert_desc* table = nullptr;   // device [n_experts + 1], entry n_experts = shared
     cx_expert_desc shared_desc{};      // host copy of the shared expert (when has_shared)
     std::vector<uint8_t> resident;     // host copy: entry i holds an expert
+    int n_resident = 0;                // routed experts held
 };
 
 namespace {
@@ -645,11 +646,12 @@ int moe_run(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int
     const bool dec = !prefill && n_tokens <= kTileTok && dec_path_ok(layer, top_k, route);
     PlanSizes z = plan_sizes(n_tokens, top_k, layer->n_experts, layer->has_shared);
     if (dec) z.max_items = z.max_slots;  // one item per slot (<= 16 pairs each)
-    // Calls with at least kBigPairs pairs per routed expert on average: the
-    // experts' weights serve hundreds of columns, so 128-pair items through
-    // the LDS-ring GEMM instead of 64-pair items that each re-stream them.
+    // Calls with at least kBigPairs pairs per resident routed expert on
+    // average (routes can only reach resident experts): the experts' weights
+    // serve hundreds of columns, so 128-pair items through the LDS-ring GEMM
+    // instead of 64-pair items that each re-stream them.
     const bool big = !dec && big_shape_ok(layer->hidden, layer->inter, in_dtype) &&
-                     (int64_t)n_tokens * top_k >= (int64_t)kBigPairs * layer->n_experts;
+                     (int64_t)n_tokens * top_k >= (int64_t)kBigPairs * std::max(1, layer->n_resident);
     if (big) {
         z.item_cap = kBigPairs;
         z.max_items = z.max_slots + (z.max_pairs + kBigPairs - 1) / kBigPairs;
@@ -1153,6 +1155,7 @@ int cx_layer_create(cx_ctx* ctx, int n_experts, const cx_expert_desc* const* exp
     L->has_shared = shared ? 1 : 0;
     L->resident.assign(n_experts, 0);
     for (int i = 0; i < n_experts; ++i) L->resident[i] = (experts && experts[i]) ? 1 : 0;
+    for (int i = 0; i < n_experts; ++i) L->n_resident += L->resident[i];
     L->shared_desc = host[n_experts];
     L->fast = fast;
     L->hidden = H;

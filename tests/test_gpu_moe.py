@@ -190,6 +190,39 @@ def test_moe_many_tokens_per_expert(gpu, oracle, H, I, E, T, K, dtype, shared):
         _free(layer, experts, sh)
 
 
+def test_many_tokens_per_resident_expert(gpu, oracle):
+    """A node's share: 4 of 16 experts resident, 160 tokens x 4 routes over
+    them (160 pairs per resident expert), so the LDS-ring GEMM serves the call
+    although 640 routes are few for all 16 slots.  Every token against the
+    oracle; the layer table's empty slots are never read."""
+    print("[moe] many tokens per resident expert", flush=True)
+    from constellation_amd.engine import Expert, Layer
+    E, H, I, T, K = 16, 1024, 512, 160, 4
+    res = [1, 5, 9, 13]
+    experts = [Expert.generate(0, 75, 0x1000 + 4 * e, hidden=H, inter=I) if e in res else None for e in range(E)]
+    layer = Layer(gpu, experts, None)
+    try:
+        cpu = [oracle.gen_expert(75, 0x1000 + 4 * e, hidden=H, inter=I) if e in res else None for e in range(E)]
+        x = gpu.gen_normal(76, 1, (T, H), 1.0, torch.bfloat16)
+        rng = np.random.default_rng(77)
+        ids = np.stack([rng.permutation(res) for _ in range(T)]).astype(np.int32)
+        wts = rng.uniform(0.05, 1.0, ids.shape).astype(np.float32)
+        y, yf = gpu.moe(layer, x, torch.from_numpy(ids).cuda(), torch.from_numpy(wts).cuda(),
+                        want_f32=True, prefill=True)
+        gpu.sync()
+        ref = _oracle_moe(oracle, cpu, None, x.float().cpu().numpy(), ids, wts)
+        yf = yf.cpu().numpy()
+        assert rel_l2(yf, ref) < 1e-5, rel_l2(yf, ref)
+        assert np.abs(yf - ref).max() < 2e-2
+        assert np.array_equal(_bits(y), oracle.encode_act(yf, BF16, "rne"))
+    finally:
+        torch.cuda.synchronize()
+        layer.close()
+        for e in experts:
+            if e is not None:
+                e.free()
+
+
 def test_planner_many_routes_vs_oracle(gpu, oracle):
     """4800 routes (1200 tokens x 4): more than the planner held in LDS as
     32-bit ids; staged as 16-bit ids with the validity bits in registers.
