@@ -15,6 +15,10 @@
 //                          handed out statically or claimed from per-XCD counters,
 //                          and k_down_comb1 over 256 / 384 / 448 / 512 tiles
 //   cx_kbench grouped      the grouped prefill kernels on the config-3-like plan
+//   cx_kbench rates        per-CU rates the LDS-ring kernels are built on, in shader
+//                          clocks (s_memtime): ds_read_b128 bytes per clock, bf16
+//                          MFMA and fp8 -> 16-bit convert issue intervals, and
+//                          whether independent converts overlap the MFMAs
 //
 // Bytes are synthetic (small finite fp8 codes, block scales 1e-3): the numbers
 // are timings, not results.  Built by constellation_amd/build.py.
@@ -677,6 +681,130 @@ int cmd_grouped(int iters) {
     return 0;
 }
 
+
+// ---------------------------------------------------------------------------
+// rates: one workgroup per CU, every wave timing a fixed loop with s_memtime
+// (the shader clock) between two barriers; the median over CUs is printed.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void k_rate_lds(int iters, unsigned long long* clk, uint32_t* sink) {
+    __shared__ __attribute__((aligned(16))) unsigned char lds[65536];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < 65536 / 4; i += 64 * NW) reinterpret_cast<uint32_t*>(lds)[i] = i;
+    __syncthreads();
+    // 16 consecutive bytes per lane: one wave instruction reads 1 KB
+    const uint32_t base = (uint32_t)(uintptr_t)lds + ((wave * 1024 + lane * 16) & 8191);
+    u32x4 x = {0, 0, 0, 0};
+    __syncthreads();
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+    for (int it = 0; it < iters; ++it) {
+        u32x4 v0, v1, v2, v3, v4, v5, v6, v7;
+        asm volatile(
+            "ds_read_b128 %0, %8\n ds_read_b128 %1, %8 offset:8192\n ds_read_b128 %2, %8 offset:16384\n"
+            "ds_read_b128 %3, %8 offset:24576\n ds_read_b128 %4, %8 offset:32768\n ds_read_b128 %5, %8 offset:40960\n"
+            "ds_read_b128 %6, %8 offset:49152\n ds_read_b128 %7, %8 offset:57344\n s_waitcnt lgkmcnt(0)"
+            : "=v"(v0), "=v"(v1), "=v"(v2), "=v"(v3), "=v"(v4), "=v"(v5), "=v"(v6), "=v"(v7)
+            : "v"(base));
+        x ^= v0 ^ v1 ^ v2 ^ v3 ^ v4 ^ v5 ^ v6 ^ v7;
+    }
+    __syncthreads();
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+    if (tid == 0) clk[blockIdx.x] = t1 - t0;
+    sink[blockIdx.x * 64 * NW + tid] = x[0] ^ x[1] ^ x[2] ^ x[3];
+}
+
+// NM independent bf16 MFMAs and NCVT independent fp8 -> bf16 converts per
+// iteration (the converts' results do not feed the MFMAs)
+template <int NW, int NM, int NCVT>
+__global__ __launch_bounds__(64 * NW) void k_rate_valu(int iters, unsigned long long* clk, uint32_t* sink) {
+    typedef Mma<false> M;
+    const int tid = threadIdx.x;
+    u32x4 ra, rb;
+    for (int i = 0; i < 4; ++i) {
+        ra[i] = 0x3f803f80u + tid;
+        rb[i] = 0x3f003f00u + i;
+    }
+    const M::V a = M::bits(ra), b = M::bits(rb);
+    f32x4 acc[8];
+    for (int j = 0; j < 8; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint32_t src[16];
+    for (int j = 0; j < 16; ++j) src[j] = 0x3c3c3c3cu + tid * 17 + j;
+    __syncthreads();
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+    for (int it = 0; it < iters; ++it) {
+        uint32_t r[16];
+#pragma unroll
+        for (int j = 0; j < (NM > NCVT ? NM : NCVT); ++j) {
+            if (j < NM) acc[j] = M::mma(a, b, acc[j]);
+            if (j < NCVT) asm volatile("v_cvt_scalef32_pk_bf16_fp8 %0, %1, %2" : "=v"(r[j]) : "v"(src[j]), "v"(1.0f));
+        }
+        if constexpr (NM > 0)
+            asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]), "+v"(acc[5]),
+                         "+v"(acc[6]), "+v"(acc[7]));
+#pragma unroll
+        for (int j = 0; j < NCVT; ++j) src[j] ^= r[j] & 1;
+    }
+    __syncthreads();
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+    float sum = 0.f;
+    for (int j = 0; j < 8; ++j) sum += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+    uint32_t x = 0;
+    for (int j = 0; j < 16; ++j) x ^= src[j];
+    if (tid == 0) clk[blockIdx.x] = t1 - t0;
+    sink[blockIdx.x * 64 * NW + tid] = __float_as_uint(sum) ^ x;
+}
+
+int cmd_rates(int iters) {
+    const int cus = n_cu();
+    const int n = 2000 * std::max(1, iters / 30);
+    unsigned long long* clk;
+    uint32_t* sink;
+    KB_CHECK(hipMalloc(&clk, sizeof(unsigned long long) * cus));
+    KB_CHECK(hipMalloc(&sink, sizeof(uint32_t) * cus * 1024));
+    hipEvent_t e0, e1;
+    KB_CHECK(hipEventCreate(&e0));
+    KB_CHECK(hipEventCreate(&e1));
+    // second launch timed (the first warms up); median shader clocks over CUs
+    auto run = [&](auto kern, int nw, double* ms) {
+        for (int rep = 0; rep < 2; ++rep) {
+            KB_CHECK(hipEventRecord(e0));
+            hipLaunchKernelGGL(kern, dim3(cus), dim3(64 * nw), 0, 0, n, clk, sink);
+            KB_CHECK(hipGetLastError());
+            KB_CHECK(hipEventRecord(e1));
+            KB_CHECK(hipEventSynchronize(e1));
+        }
+        float f;
+        KB_CHECK(hipEventElapsedTime(&f, e0, e1));
+        *ms = f;
+        std::vector<unsigned long long> h(cus);
+        KB_CHECK(hipMemcpy(h.data(), clk, sizeof(unsigned long long) * cus, hipMemcpyDeviceToHost));
+        std::sort(h.begin(), h.end());
+        return (double)h[cus / 2];
+    };
+    std::printf("%d CUs, %d loop iterations per wave; clocks are s_memtime (shader clock) counts\n", cus, n);
+    double ms, c;
+    c = run(k_rate_lds<4>, 4, &ms);
+    std::printf("ds_read_b128, 4 waves/CU     %6.1f B per clock per CU  (%.3f ms, ~%.2f GHz)\n", 4.0 * n * 8 * 1024 / c, ms, c / (ms * 1e6));
+    c = run(k_rate_lds<8>, 8, &ms);
+    std::printf("ds_read_b128, 8 waves/CU     %6.1f B per clock per CU  (%.3f ms, ~%.2f GHz)\n", 8.0 * n * 8 * 1024 / c, ms, c / (ms * 1e6));
+    c = run(k_rate_lds<16>, 16, &ms);
+    std::printf("ds_read_b128, 16 waves/CU    %6.1f B per clock per CU  (%.3f ms, ~%.2f GHz)\n", 16.0 * n * 8 * 1024 / c, ms, c / (ms * 1e6));
+    auto per = [&](double clks, int nw, int per_iter) { return clks / ((double)n * per_iter * nw / 4); };
+    c = run(k_rate_valu<4, 8, 0>, 4, &ms);
+    std::printf("bf16 MFMA 16x16x32, 1 wave/SIMD      %5.2f clocks per MFMA per SIMD\n", per(c, 4, 8));
+    c = run(k_rate_valu<8, 8, 0>, 8, &ms);
+    std::printf("bf16 MFMA 16x16x32, 2 waves/SIMD     %5.2f clocks per MFMA per SIMD  (%.0f TFLOP/s over the chip)\n", per(c, 8, 8),
+                (double)cus * 4 * ((double)n * 8 * 2) * 16 * 16 * 32 * 2 / (ms * 1e-3) / 1e12);
+    c = run(k_rate_valu<8, 0, 16>, 8, &ms);
+    std::printf("fp8->bf16 pk convert, 2 waves/SIMD   %5.2f clocks per instruction per SIMD\n", per(c, 8, 16));
+    c = run(k_rate_valu<8, 8, 4>, 8, &ms);
+    std::printf("8 MFMA + 4 converts, 2 waves/SIMD    %5.2f clocks per MFMA per SIMD\n", per(c, 8, 8));
+    c = run(k_rate_valu<8, 8, 8>, 8, &ms);
+    std::printf("8 MFMA + 8 converts, 2 waves/SIMD    %5.2f clocks per MFMA per SIMD\n", per(c, 8, 8));
+    KB_CHECK(hipFree(clk));
+    KB_CHECK(hipFree(sink));
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -687,6 +815,7 @@ int main(int argc, char** argv) {
     if (!std::strcmp(cmd, "placement")) return cmd_placement(iters);
     if (!std::strcmp(cmd, "decode-balance")) return cmd_decode_balance(iters);
     if (!std::strcmp(cmd, "grouped")) return cmd_grouped(std::min(iters, 12));
-    std::fprintf(stderr, "usage: cx_kbench layout|decode-down|placement|decode-balance|grouped [launches]\n");
+    if (!std::strcmp(cmd, "rates")) return cmd_rates(iters);
+    std::fprintf(stderr, "usage: cx_kbench layout|decode-down|placement|decode-balance|grouped|rates [launches]\n");
     return 2;
 }
