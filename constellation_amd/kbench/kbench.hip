@@ -734,15 +734,22 @@ __global__ __launch_bounds__(64 * NW) void k_rate_valu(int iters, unsigned long 
         uint32_t r[16];
 #pragma unroll
         for (int j = 0; j < (NM > NCVT ? NM : NCVT); ++j) {
-            if (j < NM) acc[j] = M::mma(a, b, acc[j]);
+            // the MFMA as written, so each accumulator stays in its own
+            // registers across iterations (AGPRs at one wave per SIMD, where
+            // the compiler otherwise rotates them through copies)
+            if (j < NM) {
+                if constexpr (NW <= 4)
+                    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc[j]) : "v"(a), "v"(b));
+                else
+                    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc[j]) : "v"(a), "v"(b));
+            }
             if (j < NCVT) asm volatile("v_cvt_scalef32_pk_bf16_fp8 %0, %1, %2" : "=v"(r[j]) : "v"(src[j]), "v"(1.0f));
         }
-        if constexpr (NM > 0)
-            asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]), "+v"(acc[5]),
-                         "+v"(acc[6]), "+v"(acc[7]));
 #pragma unroll
         for (int j = 0; j < NCVT; ++j) src[j] ^= r[j] & 1;
     }
+    // the last MFMAs' results are read below: let them retire first
+    asm volatile("s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7");
     __syncthreads();
     const unsigned long long t1 = __builtin_amdgcn_s_memtime();
     float sum = 0.f;
