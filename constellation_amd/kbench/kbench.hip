@@ -803,6 +803,10 @@ int cmd_rates(int iters) {
                 (double)cus * 4 * ((double)n * 8 * 2) * 16 * 16 * 32 * 2 / (ms * 1e-3) / 1e12);
     c = run(k_rate_valu<8, 0, 16>, 8, &ms);
     std::printf("fp8->bf16 pk convert, 2 waves/SIMD   %5.2f clocks per instruction per SIMD\n", per(c, 8, 16));
+    c = run(k_rate_valu<4, 8, 4>, 4, &ms);
+    std::printf("8 MFMA + 4 converts, 1 wave/SIMD     %5.2f clocks per MFMA per SIMD\n", per(c, 4, 8));
+    c = run(k_rate_valu<4, 8, 8>, 4, &ms);
+    std::printf("8 MFMA + 8 converts, 1 wave/SIMD     %5.2f clocks per MFMA per SIMD\n", per(c, 4, 8));
     c = run(k_rate_valu<8, 8, 4>, 8, &ms);
     std::printf("8 MFMA + 4 converts, 2 waves/SIMD    %5.2f clocks per MFMA per SIMD\n", per(c, 8, 8));
     c = run(k_rate_valu<8, 8, 8>, 8, &ms);
