@@ -1,6 +1,10 @@
 """Builds libcx_moe.so (HIP, gfx950) in-tree with hipcc.
 
-    python -m constellation_amd.build          # or constellation_amd.build.build()
+    python -m constellation_amd.build            # the library (build())
+    python -m constellation_amd.build --kbench   # the kernel micro-benchmark only
+
+The library build does not depend on the micro-benchmark: build() compiles
+libcx_moe.so alone, build_kbench() the stand-alone cx_kbench program.
 
 Every HIP file is compiled with packed-fp32 code generation disabled
 (-Xclang -target-feature -Xclang -packed-fp32-ops) and the generator with
@@ -81,10 +85,8 @@ def build_kbench(verbose: bool = False) -> Path:
 
 def build(verbose: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(5, os.cpu_count() or 1)) as ex:
-        kb = ex.submit(build_kbench, verbose)
+    with ThreadPoolExecutor(max_workers=min(4, os.cpu_count() or 1)) as ex:
         objs = list(ex.map(lambda kv: _compile(*kv), SOURCES.items()))
-        kb.result()
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -98,4 +100,7 @@ def build(verbose: bool = False) -> Path:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    if "--kbench" in sys.argv[1:]:
+        build_kbench(verbose=True)
+    else:
+        build(verbose=True)

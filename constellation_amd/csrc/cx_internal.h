@@ -91,7 +91,15 @@ enum : int {
     kErrNotResident = 2,
     kErrPlanOverflow = 4,
     kErrDuplicateRoute = 8,
+    kErrBadWeight = 16,  // negative or non-finite route weight (validate_routes, moe_layer_runtime.py:96-97)
 };
+
+// A route weight the planners accept: finite and >= 0 (validate_routes
+// rejects negative weights, server/moe_layer_runtime.py:96-97; a NaN or an
+// infinity cannot come out of the router and is rejected too).
+__device__ __forceinline__ bool route_weight_ok(float w) {
+    return w >= 0.0f && w <= 3.402823466e38f;
+}
 
 // ---------------------------------------------------------------------------
 // Kernel-duration timing.  While a LaunchTimer is current on the calling

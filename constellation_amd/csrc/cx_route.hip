@@ -710,6 +710,7 @@ __device__ __forceinline__ void plan_build(const int32_t* __restrict__ ids, cons
         if (e >= n_experts) { atomicOr(&s_err, kErrBadExpertId); continue; }
         if (table[e].w_up == nullptr) { atomicOr(&s_err, kErrNotResident); continue; }
         if (dup_route(ids, i, top_k)) { atomicOr(&s_err, kErrDuplicateRoute); continue; }
+        if (!route_weight_ok(w[i])) { atomicOr(&s_err, kErrBadWeight); continue; }
         atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
@@ -740,7 +741,8 @@ __device__ __forceinline__ void plan_build(const int32_t* __restrict__ ids, cons
         const int e = ids[i];
         const int t = i / top_k, k = i - t * top_k;
         int pos = -1;
-        if (e >= 0 && e < n_experts && table[e].w_up != nullptr && !dup_route(ids, i, top_k)) {
+        if (e >= 0 && e < n_experts && table[e].w_up != nullptr && !dup_route(ids, i, top_k) &&
+            route_weight_ok(w[i])) {
             pos = atomicAdd(&cur[e], 1);
             P.pair_token[pos] = t;
             P.pair_weight[pos] = w[i];
@@ -863,6 +865,7 @@ __device__ __forceinline__ void plan_build_staged(const int32_t* __restrict__ id
                 bool dup = false;
                 for (int j = (i / top_k) * top_k; j < i; ++j) dup |= sid[j] == e;
                 if (dup) atomicOr(&s_err, kErrDuplicateRoute);
+                else if (!route_weight_ok(ldf(w + i))) atomicOr(&s_err, kErrBadWeight);
                 else {
                     okm |= 1ull << r;
                     atomicAdd(&cnt[e], 1);
@@ -1480,6 +1483,10 @@ __global__ __launch_bounds__(kRouteThreads) void k_dec_plan_sgu(DecIdsArgs P, Ex
         } else if (ok) {
             for (int j = t * K; j < i; ++j)
                 if (rid[j] == e) { err |= kErrDuplicateRoute; ok = false; break; }
+            if (ok && !route_weight_ok(myw[r])) {
+                err |= kErrBadWeight;
+                ok = false;
+            }
         }
         if (ok) {
             atomicOr(&S.mask[t][e >> 5], 1u << (e & 31));

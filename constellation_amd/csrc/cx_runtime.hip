@@ -630,9 +630,11 @@ int moe_decode(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, 
 // Routed-expert compute; when `route` is given, the router runs first on the
 // same stream.  T <= 16 takes the decode pipeline where the shapes allow it;
 // otherwise route -> plan -> grouped gate/up -> per-pair down -> combine.
+// valid_routes: routes with an id >= 0 when the caller knows them on the
+// host (the wire entry point), else -1.
 int moe_run(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int n_tokens,
             const int32_t* ids, const float* w, int top_k, void* y, int out_dtype, float* y_f32,
-            hipStream_t s, bool prefill, RouteArgs* route) {
+            hipStream_t s, bool prefill, RouteArgs* route, int64_t valid_routes = -1) {
     if (!ctx || !layer) return fail(CX_EINVAL, "NULL context or layer");
     if (!act16(in_dtype) || !act16(out_dtype)) return fail(CX_EINVAL, "dtypes must be fp16/bf16");
     if (n_tokens <= 0 || top_k < 0 || top_k > 64) return fail(CX_EINVAL, "bad n_tokens/top_k");
@@ -647,11 +649,16 @@ int moe_run(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, int
     PlanSizes z = plan_sizes(n_tokens, top_k, layer->n_experts, layer->has_shared);
     if (dec) z.max_items = z.max_slots;  // one item per slot (<= 16 pairs each)
     // Calls with at least kBigPairs pairs per resident routed expert on
-    // average (routes can only reach resident experts): the experts' weights
-    // serve hundreds of columns, so 128-pair items through the LDS-ring GEMM
-    // instead of 64-pair items that each re-stream them.
+    // average: the experts' weights serve hundreds of columns, so 128-pair
+    // items through the LDS-ring GEMM instead of 64-pair items that each
+    // re-stream them.  The pairs are counted on the host: exactly when the
+    // caller knows its valid routes (the wire entry point), else as every
+    // route slot, an upper bound — route tables masked to one node of
+    // several (-1 for other nodes' experts) can then take the LDS-ring path
+    // with mostly-padding tiles (correct, slower).
+    const int64_t pairs = valid_routes >= 0 ? valid_routes : (int64_t)n_tokens * top_k;
     const bool big = !dec && big_shape_ok(layer->hidden, layer->inter, in_dtype) &&
-                     (int64_t)n_tokens * top_k >= (int64_t)kBigPairs * std::max(1, layer->n_resident);
+                     pairs >= (int64_t)kBigPairs * std::max(1, layer->n_resident);
     if (big) {
         z.item_cap = kBigPairs;
         z.max_items = z.max_slots + (z.max_pairs + kBigPairs - 1) / kBigPairs;
@@ -1005,11 +1012,12 @@ int cx_ctx_sync(cx_ctx* ctx, void* stream) {
     if (flag != 0) {
         CX_HIP(hipMemsetAsync(ctx->err_flag, 0, sizeof(int), s));
         CX_HIP(hipStreamSynchronize(s));
-        return fail(CX_EDEVICE, "device check failed (flags 0x%x:%s%s%s%s)", flag,
+        return fail(CX_EDEVICE, "device check failed (flags 0x%x:%s%s%s%s%s)", flag,
                     (flag & kErrBadExpertId) ? " expert id out of range" : "",
                     (flag & kErrNotResident) ? " expert not resident" : "",
                     (flag & kErrPlanOverflow) ? " plan overflow" : "",
-                    (flag & kErrDuplicateRoute) ? " expert routed twice for one token" : "");
+                    (flag & kErrDuplicateRoute) ? " expert routed twice for one token" : "",
+                    (flag & kErrBadWeight) ? " negative or non-finite route weight" : "");
     }
     return CX_OK;
 }
@@ -1284,6 +1292,7 @@ int cx_moe_layer_request_run(cx_ctx* ctx, const cx_layer* layer, const uint8_t* 
     int status = 0;
     bool any_route = false;
     bool bad_weight = false;
+    int64_t n_valid = 0;
     for (size_t i = 0; i < r.n_routes && status != 1; ++i) {
         int32_t id;
         float wt;
@@ -1291,6 +1300,7 @@ int cx_moe_layer_request_run(cx_ctx* ctx, const cx_layer* layer, const uint8_t* 
         std::memcpy(&wt, r.w + 4 * i, 4);
         if (id < 0) continue;
         any_route = true;
+        ++n_valid;
         // validate_routes (server/moe_layer_runtime.py:96-97) rejects negative
         // weights; a non-finite one cannot be combined either
         if (!(wt >= 0.0f) || wt > 3.4028234663852886e38f) bad_weight = true;
@@ -1330,7 +1340,7 @@ int cx_moe_layer_request_run(cx_ctx* ctx, const cx_layer* layer, const uint8_t* 
     rc = moe_run(ctx, &view, dx + act_off, (int)h.input_dtype, T,
                  K > 0 ? reinterpret_cast<const int32_t*>(dx) : nullptr,
                  K > 0 ? reinterpret_cast<const float*>(dx + rb) : nullptr, K, ctx->dy.p,
-                 (int)h.output_dtype, nullptr, s, T > kTileTok, nullptr);
+                 (int)h.output_dtype, nullptr, s, T > kTileTok, nullptr, n_valid);
     if (rc) {
         (void)hipStreamSynchronize(s);
         *resp_len = write_layer_resp(resp, 4, h, 0);

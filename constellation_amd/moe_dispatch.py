@@ -21,12 +21,25 @@ each node once:
     a worker port): one MoeLayerRequest (msg 42, v1 framing
     common/protocol.h:10-62) per layer, answered with the node's partial sum.
 The shared expert is folded into the first node that holds it (FLAG_SHARED).
-Partials of several nodes are added in fp32 in node order and rounded once;
-a single node's answer is returned as it is.
+Partials of several nodes are added in fp32 in node order, then rounded to
+the output dtype: a local node's partial enters the sum in fp32 (one
+rounding in all), a remote node's arrives already rounded to 16 bits by its
+node (the wire carries 16-bit activations), so a layer split across a
+remote node is rounded twice.  A single node's answer is returned as it is.
 
-Routes are validated as validate_routes does (server/moe_layer_runtime.py:
-84-98): a negative weight or an expert listed twice for one token raises
-RuntimeError with the reference's message; an empty route list raises too.
+Routes are checked as validate_routes does (server/moe_layer_runtime.py:
+84-98): an expert listed twice for one token and a negative (or
+non-finite) weight are errors.
+  * validate=True (default): the planner checks every route on the device
+    and skips a bad one; the error is raised (CxError, a RuntimeError) by
+    the context's next synchronisation — check_routes(device) or
+    engine.Context.sync() — so the call itself copies and waits for nothing.
+    When the layer is split across nodes the routes are on the host anyway
+    (each node's request is built there) and are checked there at once.
+  * validate="host": the routes are copied to the host and checked before
+    any compute, raising RuntimeError with the reference's messages ("routes
+    is empty" included).
+  * validate=False: no host-side check (the device still skips bad routes).
 """
 from __future__ import annotations
 
@@ -148,6 +161,8 @@ def validate_routes(ids: np.ndarray, w: np.ndarray) -> None:
             seen.add(e)
             if x < 0:
                 raise RuntimeError(f"negative route weight for expert {e}: {x}")
+            if not np.isfinite(x):
+                raise RuntimeError(f"non-finite route weight for expert {e}: {x}")
 
 
 def _as_2d(hidden: torch.Tensor) -> tuple[torch.Tensor, bool]:
@@ -158,9 +173,17 @@ def _as_2d(hidden: torch.Tensor) -> tuple[torch.Tensor, bool]:
     return hidden, False
 
 
+def check_routes(device: int = 0) -> None:
+    """Raises (CxError) if a route of an earlier call on this thread's context
+    of `device` failed the device-side checks (validate=True); waits for the
+    context's work on the device's current stream."""
+    _context(device).sync()
+
+
 def run_topk_moe_layer(nodes: Sequence[Node], hidden: torch.Tensor, layer_id: int,
                        topk_ids, topk_w, *, n_experts: int = 256, shared: bool = True,
-                       out_dtype: Optional[torch.dtype] = None, validate: bool = True) -> torch.Tensor:
+                       out_dtype: Optional[torch.dtype] = None,
+                       validate: Union[bool, str] = True) -> torch.Tensor:
     """Routed (and shared) expert compute of one layer for a token batch.
 
     hidden: [T, H] (or [H]) fp16/bf16 on the HIP device.  topk_ids / topk_w:
@@ -168,18 +191,20 @@ def run_topk_moe_layer(nodes: Sequence[Node], hidden: torch.Tensor, layer_id: in
     host arrays.  Returns [T, H] (or [H]) in out_dtype (default hidden's) on
     hidden's device: y[t] = sum_k w[t,k] expert_k(x[t]) (+ shared(x[t])).
     Each route goes to the first node in `nodes` that holds its expert; a
-    route no node holds raises.  `validate` copies the routes to the host
-    for validate_routes' checks (the device path itself skips duplicates)."""
+    route no node holds raises.  `validate`: see the module docstring."""
+    if validate not in (True, False, "host"):
+        raise ValueError(f"validate must be True, False or 'host', got {validate!r}")
     x, was_1d = _as_2d(hidden)
     local = any(isinstance(n, LocalNode) for n in nodes)
     dev = _hip_device(x) if local else None
     out_dtype = out_dtype or x.dtype
     ids_d = torch.as_tensor(topk_ids, device=x.device).to(torch.int32).reshape(x.shape[0], -1)
     w_d = torch.as_tensor(topk_w, device=x.device).to(torch.float32).reshape(x.shape[0], -1)
-    if (not validate and len(nodes) == 1 and local and layer_id in nodes[0].layers
+    if (validate != "host" and len(nodes) == 1 and local and layer_id in nodes[0].layers
             and (nodes[0].layers[layer_id].shared is not None) == shared):
-        # one local node: routes stay on the device; a route to an expert that
-        # is not resident is skipped and reported by the device check
+        # one local node: routes stay on the device; the planner skips and
+        # flags a route to an expert that is not resident, a repeated expert
+        # and a bad weight (raised by the context's next sync)
         ctx = _context(dev)
         with torch.cuda.device(dev):
             y = ctx.moe(nodes[0].layers[layer_id], x, ids_d, w_d, out_dtype=out_dtype)
@@ -214,17 +239,19 @@ def run_topk_moe_layer(nodes: Sequence[Node], hidden: torch.Tensor, layer_id: in
                 raise RuntimeError("a local layer with a shared expert must serve the shared expert "
                                    "(list its node first)")
             with torch.cuda.device(dev):
-                y = ctx.moe(lay, x, sel_d, w_d, out_dtype=out_dtype)
-            partials.append(y)
+                # a partial that is summed with others stays fp32 until the end
+                y, yf = ctx.moe(lay, x, sel_d, w_d, out_dtype=out_dtype, want_f32=True)
+            partials.append((y, yf))
         else:
-            partials.append(node.call(layer_id, x, sel, w_d.cpu().numpy(), n_i == shared_node,
-                                      out_dtype))
+            y = node.call(layer_id, x, sel, w_d.cpu().numpy(), n_i == shared_node, out_dtype)
+            partials.append((y, None))
     if len(partials) == 1:
-        y = partials[0]
+        y = partials[0][0]
     else:
-        acc = partials[0].float()
-        for p in partials[1:]:
-            acc = acc + p.float()
+        acc = None
+        for y16, y32 in partials:
+            part = y32 if y32 is not None else y16.float()
+            acc = part.clone() if acc is None else acc + part
         y = acc.to(out_dtype)
     return y.view(-1) if was_1d else y
 

@@ -248,3 +248,320 @@ def _route_aux(logits64, bias, resident, *, n_group: int, topk_group: int,
         "effective_top_k": k,
         "routes": routes,
     }
+
+
+# ---------------------------------------------------------------------------
+# Session-level drop-ins for the reference's expert dispatch
+# (server/moe_layer_runtime.py:84-98, 170-229, 411-578).
+#
+# The session is the reference's InferenceSession (server/inference_session.py:
+# 22-60): `coord.placements` (dicts with "expert_id" (global), "host",
+# "worker_port"), `client_pool.get(host, port)` / `.invalidate(host, port)`
+# returning a connected NodeClient (server/client.py: send_message /
+# recv_message), `cfg["run"]["experts_per_layer"]`, and for run_moe_layer
+# `backbone_store` and `get_router_config()`.  One optional attribute is
+# read: `cx_local_nodes`, a dict (host, worker_port) -> moe_dispatch.LocalNode
+# for the placement endpoints whose experts live on this process's GPU; their
+# routes run on the device with no host copy.  Every other endpoint gets one
+# MoeLayerRequest (msg 42) per layer through the session's client pool,
+# instead of one InferRequest per expert.
+
+def validate_routes(routes):
+    """validate_routes (server/moe_layer_runtime.py:84-98): the same checks
+    and messages over a list of (expert_id, weight)."""
+    if not routes:
+        raise RuntimeError("routes is empty")
+    seen = set()
+    for expert_id, weight in routes:
+        expert_id = int(expert_id)
+        weight = float(weight)
+        if expert_id in seen:
+            raise RuntimeError(f"duplicate expert_id in routes: {expert_id}")
+        seen.add(expert_id)
+        if weight < 0:
+            raise RuntimeError(f"negative route weight for expert {expert_id}: {weight}")
+
+
+def _experts_per_layer(session) -> int:
+    cfg = getattr(session, "cfg", None) or {}
+    run = cfg.get("run") or {}
+    return int(run.get("experts_per_layer", 256))
+
+
+def _placement(placements, expert_id: int):
+    """find_expert_placement (server/expert_placement.py:53-58)."""
+    for p in placements:
+        if int(p["expert_id"]) == expert_id:
+            return p
+    raise RuntimeError(f"expert {expert_id} not found in placements")
+
+
+def _wire_dtype(dtype: torch.dtype) -> torch.dtype:
+    """16-bit activation dtype of a request: hidden's own when it is 16-bit,
+    else fp16, the dtype the reference's wire carries (moe_layer_runtime.py:
+    36, 41-48)."""
+    return dtype if dtype in (torch.float16, torch.bfloat16) else torch.float16
+
+
+def _remote_layer_call(session, host: str, port: int, layer_id: int, x16: torch.Tensor,
+                       local_ids, weights, out16: torch.dtype) -> torch.Tensor:
+    """One MoeLayerRequest through the session's NodeClient for (host, port);
+    returns the node's weighted partial [1, H] (out16) on the host.  On a
+    transport error the connection is invalidated and the error re-raised,
+    as infer_one_expert does (moe_layer_runtime.py:37-53)."""
+    import numpy as np
+
+    from . import moe_layer_protocol as P
+    from .moe_dispatch import _RID
+
+    H = int(x16.shape[-1])
+    K = len(local_ids)
+    body = P.encode_moe_layer_request({
+        "layer_id": layer_id, "batch_size": 1, "hidden_dim": H, "top_k": K,
+        "input_dtype": engine.cx_dtype(x16.dtype), "output_dtype": engine.cx_dtype(out16),
+        "flags": 0, "expert_ids": np.asarray([local_ids], np.int32),
+        "expert_weights": np.asarray([weights], np.float32),
+        "activation": x16.contiguous().cpu().view(torch.int16).numpy().tobytes()})
+    pool = session.client_pool
+    rid = next(_RID) & 0xFFFFFFFF
+    try:
+        client = pool.get(host, port)
+        client.send_message(P.MOE_LAYER_REQUEST, rid, body)
+        msg = client.recv_message()
+    except Exception:
+        pool.invalidate(host, port)
+        raise
+    hdr = msg["header"]
+    if int(hdr["msg_type"]) != P.MOE_LAYER_RESPONSE or int(hdr["request_id"]) != rid:
+        raise P.ProtocolError(
+            f"unexpected reply type={int(hdr['msg_type'])} rid={int(hdr['request_id'])}")
+    resp = P.decode_moe_layer_response(msg["body"])
+    if resp["status_code"] != 0:
+        raise RuntimeError(
+            f"moe layer {layer_id} failed on node {host}:{port}: status={resp['status_code']}")
+    if resp["batch_size"] != 1 or resp["hidden_dim"] != H or len(resp["output"]) != H * 2:
+        raise RuntimeError(
+            f"unexpected moe layer output size from node {host}:{port}: "
+            f"got={len(resp['output'])} bytes expected={H * 2}")
+    return torch.frombuffer(bytearray(resp["output"]), dtype=torch.int16).view(out16).view(1, H)
+
+
+def run_topk_moe_layer(session, hidden, routes, *, return_aux: bool = False,
+                       accum_dtype: torch.dtype = torch.float32):
+    """Drop-in for run_topk_moe_layer (server/moe_layer_runtime.py:170-229):
+    same signature, checks and return shape.
+
+    hidden: 1-D tensor (the reference passes the fp32 router input);
+    routes: [(global_expert_id, weight)] as run_moe_layer builds them.
+    Returns (combined, weighted_outputs), or (combined, weighted_outputs,
+    expert_outputs) with return_aux.  combined = sum_k w_k y_k accumulated in
+    `accum_dtype` and cast to hidden's dtype, on hidden's device (the
+    reference's is on the CPU).
+
+    Routes are grouped by the placement endpoint that serves them and by
+    layer.  Without return_aux each group is ONE request carrying all its
+    routes and weights (MoeLayerRequest to a remote node, the device path for
+    a `cx_local_nodes` endpoint): the node returns its weighted partial sum,
+    so `weighted_outputs` holds one entry per node request,
+    (-1, 1.0, partial) with partial an fp32 tensor on hidden's device —
+    outputs are per node, not per expert.  With return_aux, every route is
+    its own request of weight 1.0 (as the reference's diagnostics need each
+    expert's output): `weighted_outputs` is [(expert_id, weight, y)] and
+    `expert_outputs` the reference's per-expert dicts, with y the expert's
+    16-bit output widened to fp32 numpy, as infer_one_expert returns it."""
+    import numpy as np
+
+    from .moe_dispatch import LocalNode
+
+    if not isinstance(hidden, torch.Tensor):
+        raise TypeError(f"hidden must be torch.Tensor, got {type(hidden).__name__}")
+    if hidden.ndim != 1:
+        raise RuntimeError(f"hidden must be 1D, got shape={tuple(hidden.shape)}")
+    validate_routes(routes)
+    routes = [(int(e), float(w)) for e, w in routes]
+    hidden = hidden.detach()
+    out_dtype = hidden.dtype
+    x16 = hidden.to(_wire_dtype(hidden.dtype)).contiguous().view(1, -1)
+    epl = _experts_per_layer(session)
+    local_nodes = getattr(session, "cx_local_nodes", None) or {}
+    # group by (endpoint, layer) in first-appearance order
+    groups: dict = {}
+    for gid, w in routes:
+        p = _placement(session.coord.placements, gid)
+        key = (str(p["host"]), int(p["worker_port"]), gid // epl)
+        groups.setdefault(key, []).append((gid, w))
+
+    def run_group(host, port, layer_id, members, unit_weights):
+        ids = [gid % epl for gid, _ in members]
+        wts = [1.0 if unit_weights else w for _, w in members]
+        node = local_nodes.get((host, port))
+        if node is not None:
+            if not isinstance(node, LocalNode) or layer_id not in node.layers:
+                raise RuntimeError(f"no local layer {layer_id} for endpoint {host}:{port}")
+            dev = _hip_device(x16)
+            ctx = _context(dev)
+            with torch.cuda.device(dev):
+                ids_d = torch.tensor([ids], dtype=torch.int32, device=x16.device)
+                w_d = torch.tensor([wts], dtype=torch.float32, device=x16.device)
+                y16, yf = ctx.moe(node.layers[layer_id], x16, ids_d, w_d,
+                                  out_dtype=x16.dtype, want_f32=True)
+            return y16, yf
+        y16 = _remote_layer_call(session, host, port, layer_id, x16, ids, wts, x16.dtype)
+        return y16, None
+
+    if not return_aux:
+        weighted_outputs = []
+        combined = None
+        for (host, port, layer_id), members in groups.items():
+            y16, yf = run_group(host, port, layer_id, members, unit_weights=False)
+            part = (yf if yf is not None else y16.float()).view(-1).to(hidden.device)
+            weighted_outputs.append((-1, 1.0, part))
+            combined = part.to(accum_dtype).clone() if combined is None else combined + part.to(accum_dtype)
+        return combined.to(out_dtype), weighted_outputs
+
+    weighted_outputs, expert_outputs = [], []
+    combined = None
+    for (host, port, layer_id), members in groups.items():
+        for gid, w in members:
+            y16, _ = run_group(host, port, layer_id, [(gid, w)], unit_weights=True)
+            y = y16.view(-1).float().cpu().numpy()
+            weighted_outputs.append((gid, w, y))
+            expert_outputs.append({
+                "expert_id": gid,
+                "weight": w,
+                "output": y.copy(),
+                "weighted_output": (w * y).astype(np.float32, copy=False),
+                "output_dtype": engine.cx_dtype(x16.dtype),
+            })
+    # combine_outputs_torch (moe_layer_runtime.py:148-167): in route order
+    order = {gid: i for i, (gid, _) in enumerate(routes)}
+    for gid, w, y in sorted(weighted_outputs, key=lambda r: order[r[0]]):
+        term = torch.as_tensor(w, dtype=accum_dtype) * torch.as_tensor(y, dtype=accum_dtype)
+        combined = term if combined is None else combined + term
+    weighted_outputs.sort(key=lambda r: order[r[0]])
+    expert_outputs.sort(key=lambda r: order[r["expert_id"]])
+    return combined.to(out_dtype).to(hidden.device), weighted_outputs, expert_outputs
+
+
+def _as_vector(x, name: str, dtype: torch.dtype, device: str) -> torch.Tensor:
+    """as_array(x, name, ARRCFG_VECTOR_TORCH(dtype, device))
+    (server/array_utils.py:61-73, 154-213): a 1-D, finite, contiguous torch
+    tensor of exactly `dtype` on `device`; no cast or move."""
+    if not isinstance(x, torch.Tensor):
+        raise TypeError(f"{name} expected torch backend, got type={type(x).__name__}")
+    if x.ndim != 1:
+        raise ValueError(f"{name} must have ndim in [1], got shape {tuple(int(v) for v in x.shape)}")
+    if x.shape[-1] == 0:
+        raise ValueError(
+            f"{name} must not have empty hidden dimension, got shape {tuple(int(v) for v in x.shape)}")
+    if x.dtype != dtype:
+        raise TypeError(f"{name} expected dtype={dtype}, got dtype={x.dtype}")
+    if str(x.device) != str(device):
+        raise RuntimeError(f"{name} expected device={device}, got device={x.device}")
+    if not torch.all(torch.isfinite(x)).item():
+        raise ValueError(f"{name} contains non-finite values")
+    return x.contiguous()
+
+
+def run_moe_layer(session, hidden, layer_id: int, *, return_aux: bool = False):
+    """Drop-in for run_moe_layer (server/moe_layer_runtime.py:411-578): the
+    same checks, resident-expert selection, router call, global ids and
+    result dict ({"output": ...} plus "aux" with return_aux), with the HIP
+    router (route_token_real above) and run_topk_moe_layer above (one
+    request per node instead of one per expert).  gate_weight may be fp32,
+    as the reference requires, or the checkpoint's bf16."""
+    layer_id = int(layer_id)
+    if session.backbone_store is None:
+        raise RuntimeError("session.backbone_store is not initialized")
+    layer_entry = session.backbone_store.layer(layer_id)
+    dev = str(layer_entry["device"])
+    runtime_dtype = session.backbone_store.dtype
+    hidden = _as_vector(hidden, f"moe.layer{layer_id}.hidden", runtime_dtype, dev)
+    router_cfg = session.get_router_config()
+    hidden_size = int(router_cfg["hidden_size"])
+    if int(hidden.shape[0]) != hidden_size:
+        raise RuntimeError(
+            f"hidden size mismatch: got={int(hidden.shape[0])} expected={hidden_size}")
+    if "router" not in layer_entry:
+        raise RuntimeError(f"router weights are not loaded for layer {layer_id}")
+    router_entry = layer_entry["router"]
+    gate_weight = router_entry["gate_weight"]
+    e_score_correction_bias = router_entry["e_score_correction_bias"]
+    if not isinstance(gate_weight, torch.Tensor):
+        raise TypeError(f"gate_weight must be torch.Tensor, got {type(gate_weight).__name__}")
+    if not isinstance(e_score_correction_bias, torch.Tensor):
+        raise TypeError(
+            "e_score_correction_bias must be torch.Tensor, got "
+            f"{type(e_score_correction_bias).__name__}")
+    if str(gate_weight.device) != dev:
+        raise RuntimeError(
+            f"router gate_weight expected device={dev}, got device={gate_weight.device}")
+    if str(e_score_correction_bias.device) != dev:
+        raise RuntimeError(
+            f"router bias expected device={dev}, got device={e_score_correction_bias.device}")
+    if gate_weight.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"router gate_weight must be float32, got {gate_weight.dtype}")
+    if e_score_correction_bias.dtype != torch.float32:
+        raise TypeError(
+            f"router e_score_correction_bias must be float32, got {e_score_correction_bias.dtype}")
+    router_hidden = hidden.to(dtype=torch.float32)
+    experts_per_layer = int(session.cfg["run"]["experts_per_layer"])
+    restricted = session.cfg["run"].get("restricted_expert_ids")
+    if restricted is not None:
+        resident = sorted({int(e) for e in restricted})
+        max_local = int(router_cfg["n_routed_experts"])
+        for eid in resident:
+            if eid < 0 or eid >= max_local:
+                raise RuntimeError(
+                    f"restricted expert id out of range for layer {layer_id}: "
+                    f"{eid} not in [0, {max_local})")
+    else:
+        # allowed_local_expert_ids_for_layer (server/expert_placement.py:27-43)
+        resident = sorted({int(p["expert_id"]) % experts_per_layer
+                           for p in session.coord.placements
+                           if int(p["expert_id"]) // experts_per_layer == layer_id})
+    if not resident:
+        raise RuntimeError(f"no resident experts found for layer {layer_id}")
+    kw = dict(n_group=int(router_cfg["n_group"]), topk_group=int(router_cfg["topk_group"]),
+              top_k=min(int(router_cfg["top_k"]), len(resident)),
+              norm_topk_prob=bool(router_cfg["norm_topk_prob"]),
+              routed_scaling_factor=float(router_cfg["routed_scaling_factor"]),
+              scoring_func=str(router_cfg["scoring_func"]),
+              topk_method=str(router_cfg["topk_method"]),
+              n_routed_experts=int(router_cfg["n_routed_experts"]),
+              hidden_size=int(router_cfg["hidden_size"]), resident_expert_ids=resident)
+    if return_aux:
+        routes, aux = route_token_real(router_hidden, gate_weight, e_score_correction_bias,
+                                       return_aux=True, **kw)
+    else:
+        routes = route_token_real(router_hidden, gate_weight, e_score_correction_bias, **kw)
+        aux = None
+    # make_global_expert_id (server/expert_placement.py:4-25)
+    global_routes = [(layer_id * experts_per_layer + int(e), w) for e, w in routes]
+    if return_aux:
+        combined, weighted_outputs, expert_outputs = run_topk_moe_layer(
+            session, router_hidden, global_routes, return_aux=True)
+    else:
+        combined, weighted_outputs = run_topk_moe_layer(
+            session, router_hidden, global_routes, return_aux=False)
+        expert_outputs = None
+    combined_t = torch.as_tensor(combined, dtype=runtime_dtype, device=dev)
+    combined_t = _as_vector(combined_t, f"moe.layer{layer_id}.output", runtime_dtype, dev)
+    if not return_aux:
+        return {"output": combined_t}
+    return {
+        "output": combined_t,
+        "aux": {
+            "layer_id": layer_id,
+            "router_hidden": router_hidden.detach().float().cpu().numpy(),
+            **aux,
+            "resident_local_expert_ids": resident,
+            "routes": global_routes,
+            "local_routes": routes,
+            "selected_global_expert_ids": [int(e) for e, _ in global_routes],
+            "selected_weights": [float(w) for _, w in global_routes],
+            "weighted_outputs": weighted_outputs,
+            "combined_pre_cast": torch.as_tensor(combined).detach().float().cpu().numpy(),
+            "expert_outputs": expert_outputs,
+        },
+    }

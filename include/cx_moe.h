@@ -221,10 +221,11 @@ CX_API int cx_route_logits(cx_ctx* ctx, double* out, int n_tokens, int n_experts
  * last) — a3+a4+a5+a9..a12 of the reference's decode path
  * (moe_layer_runtime.py:111-167, deepseek_full_model_executor.py:264-316,
  * full_model_runtime.py:348).  Negative ids are skipped; an id that is out
- * of range or not resident sets the context's device error (reported by
- * cx_ctx_sync) and is skipped.  Route weights are used as given (the
- * device-pointer entry points do not inspect them; the wire entry point
- * cx_moe_layer_request_run rejects negative and non-finite ones).
+ * of range or not resident, an expert listed twice for one token, and a
+ * negative or non-finite route weight (the checks of validate_routes,
+ * server/moe_layer_runtime.py:84-98) set the context's device error
+ * (reported by cx_ctx_sync) and the route is skipped.  The checks run in the
+ * planner on the device, so no route ever travels to the host.
  * cx_moe_decode targets n_tokens <= 16 per launch set;
  * cx_moe_prefill targets larger chunks (grouped MFMA GEMM tiles of 16
  * tokens, up to 64 tokens per work item).  Both accept any n_tokens. */

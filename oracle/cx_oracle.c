@@ -16,6 +16,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define CXO_API __attribute__((visibility("default")))
@@ -300,6 +301,76 @@ CXO_API void cxo_gen_fp8_matrix(uint64_t seed, uint64_t stream, int rows, int co
  * x is already decoded to fp32 (DecodeActivationToFloatV2 is exact); y is
  * returned pre-cast.  Rows are independent, so the row loop is parallel;
  * each row's sum keeps the sequential order. */
+/* x [n_tokens][len] -> blocks of tb tokens, k-major: out[(b*len + k)*tb + t]
+ * (zeros for the padding tokens of the last block). */
+static float* cxo_token_blocks(const float* x, int n_tokens, int len, int tb) {
+    const int nb = (n_tokens + tb - 1) / tb;
+    float* out = (float*)calloc((size_t)nb * len * tb, sizeof(float));
+    if (!out) return NULL;
+    for (int t = 0; t < n_tokens; ++t) {
+        const int b = t / tb, tt = t % tb;
+        for (int k = 0; k < len; ++k) out[((size_t)b * len + k) * tb + tt] = x[(size_t)t * len + k];
+    }
+    return out;
+}
+
+/* Gate/up rows [r0, r1) for token block b (TB tokens, k-major xk): h of the
+ * block's real tokens into h [T][inter] and hb (k-major, as the down reads). */
+static inline __attribute__((always_inline)) void cxo_gu_row(
+    const uint8_t* wu, const float* su_r, const uint8_t* wg, const float* sg_r, const float* lut,
+    int hidden, int inter, int up_cb, int gate_cb, const float* xk, int r, int b, int n_tokens,
+    float* h, float* hb, const int TB) {
+    const size_t base = (size_t)r * hidden;
+    float up[16], gate[16];
+    for (int t = 0; t < TB; ++t) up[t] = gate[t] = 0.0f;
+    int k = 0;
+    while (k < hidden) {
+        const int ku = (k / up_cb + 1) * up_cb, kg = (k / gate_cb + 1) * gate_cb;
+        const int kend = ku < kg ? (ku < hidden ? ku : hidden) : (kg < hidden ? kg : hidden);
+        const float s_u = su_r[k / up_cb], s_g = sg_r[k / gate_cb];
+        for (; k < kend; ++k) {
+            const float wuv = lut[wu[base + k]] * s_u;
+            const float wgv = lut[wg[base + k]] * s_g;
+            const float* xv = xk + (size_t)k * TB;
+            for (int t = 0; t < TB; ++t) {
+                const float pu = wuv * xv[t];
+                const float pg = wgv * xv[t];
+                up[t] = up[t] + pu;
+                gate[t] = gate[t] + pg;
+            }
+        }
+    }
+    for (int t = 0; t < TB && b * TB + t < n_tokens; ++t) {
+        const float silu = gate[t] / (1.0f + expf(-gate[t]));
+        const float hv = silu * up[t];
+        h[(size_t)(b * TB + t) * inter + r] = hv;
+        hb[((size_t)b * inter + r) * TB + t] = hv;
+    }
+}
+
+static inline __attribute__((always_inline)) void cxo_down_row(
+    const uint8_t* wd, const float* sd_r, const float* lut, int hidden, int inter, int down_cb,
+    const float* hk, int r, int b, int n_tokens, float* y, const int TB) {
+    const size_t base = (size_t)r * inter;
+    float sum[16];
+    for (int t = 0; t < TB; ++t) sum[t] = 0.0f;
+    int k = 0;
+    while (k < inter) {
+        const int kd = (k / down_cb + 1) * down_cb;
+        const int kend = kd < inter ? kd : inter;
+        const float s_d = sd_r[k / down_cb];
+        for (; k < kend; ++k) {
+            const float w = lut[wd[base + k]] * s_d;
+            const float* hv = hk + (size_t)k * TB;
+            for (int t = 0; t < TB; ++t) {
+                const float pr = w * hv[t];
+                sum[t] = sum[t] + pr;
+            }
+        }
+    }
+    for (int t = 0; t < TB && b * TB + t < n_tokens; ++t) y[(size_t)(b * TB + t) * hidden + r] = sum[t];
+}
+
 CXO_API void cxo_expert_ref(const uint8_t* wu, const float* su,
                             const uint8_t* wg, const float* sg,
                             const uint8_t* wd, const float* sd,
@@ -307,42 +378,50 @@ CXO_API void cxo_expert_ref(const uint8_t* wu, const float* su,
                             int up_rb, int up_cb, int gate_rb, int gate_cb,
                             int down_rb, int down_cb,
                             const float* x, int n_tokens, float* h, float* y) {
+    /* Each (token, row) value is the reference's sequence of fp32 operations
+     * (w = lut[b]*scale, p = w*x[k], sum = sum + p, k ascending); the loops
+     * only decode each weight once per block of tokens and read each column
+     * block's scale once, which changes no rounding. */
     float lut[256];
     for (int i = 0; i < 256; ++i) lut[i] = cxo_fp8_decode((uint8_t)i);
     const int up_ncb = (hidden + up_cb - 1) / up_cb;
     const int gate_ncb = (hidden + gate_cb - 1) / gate_cb;
     const int down_ncb = (inter + down_cb - 1) / down_cb;
-    for (int t = 0; t < n_tokens; ++t) {
-        const float* xt = x + (size_t)t * hidden;
-        float* ht = h + (size_t)t * inter;
+    const int tb = n_tokens >= 16 ? 16 : n_tokens >= 4 ? 4 : 1;
+    const int nb = (n_tokens + tb - 1) / tb;
+    float* xb = cxo_token_blocks(x, n_tokens, hidden, tb);
+    float* hb = (float*)calloc((size_t)nb * inter * tb, sizeof(float));
+    if (!xb || !hb) {
+        free(xb);
+        free(hb);
+        return;
+    }
 #pragma omp parallel for schedule(static)
-        for (int r = 0; r < inter; ++r) {
-            float up = 0.0f, gate = 0.0f;
-            const size_t base = (size_t)r * hidden;
-            for (int k = 0; k < hidden; ++k) {
-                const float wuv = lut[wu[base + k]] * su[(r / up_rb) * up_ncb + k / up_cb];
-                const float wgv = lut[wg[base + k]] * sg[(r / gate_rb) * gate_ncb + k / gate_cb];
-                const float pu = wuv * xt[k];
-                const float pg = wgv * xt[k];
-                up = up + pu;
-                gate = gate + pg;
-            }
-            const float silu = gate / (1.0f + expf(-gate));
-            ht[r] = silu * up;
-        }
-        float* yt = y + (size_t)t * hidden;
-#pragma omp parallel for schedule(static)
-        for (int r = 0; r < hidden; ++r) {
-            float sum = 0.0f;
-            const size_t base = (size_t)r * inter;
-            for (int k = 0; k < inter; ++k) {
-                const float w = lut[wd[base + k]] * sd[(r / down_rb) * down_ncb + k / down_cb];
-                const float p = w * ht[k];
-                sum = sum + p;
-            }
-            yt[r] = sum;
+    for (int r = 0; r < inter; ++r) {
+        const float* su_r = su + (size_t)(r / up_rb) * up_ncb;
+        const float* sg_r = sg + (size_t)(r / gate_rb) * gate_ncb;
+        for (int b = 0; b < nb; ++b) {
+            const float* xk = xb + (size_t)b * hidden * tb;
+            if (tb == 16)
+                cxo_gu_row(wu, su_r, wg, sg_r, lut, hidden, inter, up_cb, gate_cb, xk, r, b, n_tokens, h, hb, 16);
+            else if (tb == 4)
+                cxo_gu_row(wu, su_r, wg, sg_r, lut, hidden, inter, up_cb, gate_cb, xk, r, b, n_tokens, h, hb, 4);
+            else
+                cxo_gu_row(wu, su_r, wg, sg_r, lut, hidden, inter, up_cb, gate_cb, xk, r, b, n_tokens, h, hb, 1);
         }
     }
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < hidden; ++r) {
+        const float* sd_r = sd + (size_t)(r / down_rb) * down_ncb;
+        for (int b = 0; b < nb; ++b) {
+            const float* hk = hb + (size_t)b * inter * tb;
+            if (tb == 16) cxo_down_row(wd, sd_r, lut, hidden, inter, down_cb, hk, r, b, n_tokens, y, 16);
+            else if (tb == 4) cxo_down_row(wd, sd_r, lut, hidden, inter, down_cb, hk, r, b, n_tokens, y, 4);
+            else cxo_down_row(wd, sd_r, lut, hidden, inter, down_cb, hk, r, b, n_tokens, y, 1);
+        }
+    }
+    free(xb);
+    free(hb);
 }
 
 /* ------------------------------------------------------------------------- */

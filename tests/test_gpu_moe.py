@@ -277,8 +277,8 @@ def test_planner_beyond_staging_matches_chunks(gpu, oracle):
 def test_full_size_many_tokens_per_expert(gpu, oracle):
     """DeepSeek-V3 shapes (H=7168, I=2048) through the LDS-ring GEMM: 8
     routed experts + shared, 256 tokens x 4 routes (128 pairs per expert on
-    average).  A token sample against the oracle, every token against the
-    decode pipeline."""
+    average).  Every token against the oracle fed the device-resident
+    weights, and against the decode pipeline."""
     print("[moe] full-size many tokens per expert", flush=True)
     E, H, T, K = 8, 7168, 256, 4
     from constellation_amd.engine import Expert, Layer
@@ -293,15 +293,11 @@ def test_full_size_many_tokens_per_expert(gpu, oracle):
         ids_d, wts_d = torch.from_numpy(ids).cuda(), torch.from_numpy(wts).cuda()
         y, yf = gpu.moe(layer, x, ids_d, wts_d, want_f32=True, prefill=True)
         gpu.sync()
-        sel = np.array([0, 1, 77, 128, 200, 255])
-        cpu = {e: oracle.gen_expert(71, 0x5000 + 4 * e) for e in sorted(set(ids[sel].ravel().tolist()))}
-        cpu_sh = oracle.gen_expert(71, 0x5000 + 4 * E)
-        ref = _oracle_moe(oracle, [cpu.get(e) for e in range(E)], cpu_sh,
-                          x.float().cpu().numpy()[sel], ids[sel], wts[sel])
-        got = yf.cpu().numpy()[sel]
-        assert rel_l2(got, ref) < 1e-5, rel_l2(got, ref)
+        ref = _oracle_moe_all_tokens(oracle, experts, sh, x.float().cpu().numpy(), ids, wts)
+        got = yf.cpu().numpy()
+        assert rel_l2(got, ref) < 1e-5, rel_l2(got, ref)  # all 256 tokens
         assert np.abs(got - ref).max() < 2e-2
-        assert np.array_equal(_bits(y)[sel], oracle.encode_act(got, BF16, "rne"))
+        assert np.array_equal(_bits(y), oracle.encode_act(got, BF16, "rne"))
         _decode_paths_agree(gpu, layer, x, ids_d, wts_d, yf)
     finally:
         _free(layer, experts, sh)
@@ -613,13 +609,37 @@ def test_full_size_moe_layer_run_to_run_exact(gpu, oracle, T):
         _free(layer, experts, sh)
 
 
-def _sample_tokens(ids, T, n_hot=4, n_spread=4):
-    """The hottest expert's first n_hot tokens plus n_spread evenly spread ones."""
-    flat = ids[ids >= 0]
-    hot = int(np.bincount(flat).argmax())
-    hot_tok = [t for t in range(T) if hot in ids[t]][:n_hot]
-    spread = [int(v) for v in np.linspace(0, T - 1, n_spread)]
-    return sorted(set(hot_tok + spread))
+def _oracle_moe_all_tokens(oracle, experts, shared, x_f32, ids, wts):
+    """Every token against the oracle (cxo_expert_ref), fed the weights the
+    device holds (Expert.download(); the generator tests hold them
+    bit-identical to the oracle's own generator), one expert at a time: each
+    (token, route) output y_k, then the combine_outputs_torch order
+    (moe_layer_runtime.py:148-167), sum_k w_k * y_k in fp32 in route order,
+    and the shared expert added last (full_model_runtime.py:348)."""
+    T, H = x_f32.shape
+    K = ids.shape[1]
+    yk = np.zeros((T, K, H), np.float32)
+    for e in sorted(set(ids[ids >= 0].tolist())):
+        tk = np.argwhere(ids == e)
+        _, y = oracle.expert_ref(experts[e].download(), x_f32[tk[:, 0]])
+        yk[tk[:, 0], tk[:, 1]] = y
+    out = np.zeros((T, H), np.float32)
+    for t in range(T):
+        acc = np.zeros(H, np.float32)
+        for k in range(K):
+            if ids[t, k] >= 0:
+                acc = acc + np.float32(wts[t, k]) * yk[t, k]
+        out[t] = acc
+    if shared is not None:
+        out = out + oracle.expert_ref(shared.download(), x_f32)[1]
+    return out
+
+
+def _downloaded_equals_generated(oracle, expert, seed, stream_base):
+    """The device bytes of one expert equal the oracle generator's."""
+    got, want = expert.download(), oracle.gen_expert(seed, stream_base)
+    for k in ("w_up", "s_up", "w_gate", "s_gate", "w_down", "s_down"):
+        assert np.array_equal(got[k], want[k]), k
 
 
 def _decode_paths_agree(gpu, layer, x, ids, wts, yf_grouped):
@@ -648,9 +668,9 @@ def test_config3_prefill_chunk_matches_oracle(gpu, oracle):
     """The config-3 benchmark call: 512 tokens through cx_moe_layer with a
     Zipf-skewed correction bias, 256 experts + shared at DeepSeek-V3 shapes
     (hot experts split into several 64-pair items).  Every token's routes
-    against the oracle; the output of a token sample that includes the hottest
-    expert's tokens against the dequantise-then-fp32 oracle; every token
-    against the decode pipeline."""
+    against the oracle; every token's output against the dequantise-then-fp32
+    oracle fed the device-resident weights, and against the decode pipeline;
+    the 16-bit output equals RNE of the fp32 output."""
     print("[moe] config-3 prefill chunk", flush=True)
     E, H, T = 256, 7168, 512
     from constellation_amd.engine import Expert, Layer
@@ -668,16 +688,15 @@ def test_config3_prefill_chunk_matches_oracle(gpu, oracle):
             if min(margins) > 1e-12:
                 assert idn[t].tolist() == oi.tolist(), t
                 assert np.allclose(wn[t], ow, rtol=1e-6, atol=0), t
-        sample = _sample_tokens(idn, T)
-        used = sorted(set(idn[sample].ravel().tolist()) - {-1})
-        cpu = {e: oracle.gen_expert(85, 0x6000 + 4 * e) for e in used}
-        cpu_sh = oracle.gen_expert(85, 0x6000 + 4 * E)
-        ref = _oracle_moe(oracle, [cpu.get(e) for e in range(E)], cpu_sh,
-                          x.float().cpu().numpy()[sample], idn[sample], wn[sample])
-        got = yf.cpu().numpy()[sample]
-        assert rel_l2(got, ref) < 1e-5 and np.abs(got - ref).max() < 2e-2
-        assert np.array_equal(_bits(y)[sample], oracle.encode_act(got, BF16, "rne"))
-        _decode_paths_agree(gpu, layer, x, ids, wts, yf)  # all 512 tokens
+        hot = int(np.bincount(idn[idn >= 0]).argmax())
+        _downloaded_equals_generated(oracle, experts[hot], 85, 0x6000 + 4 * hot)
+        ref = _oracle_moe_all_tokens(oracle, experts, sh, x.float().cpu().numpy(), idn, wn)
+        got = yf.cpu().numpy()
+        assert rel_l2(got, ref) < 1e-5 and np.abs(got - ref).max() < 2e-2  # all 512 tokens
+        for t in range(T):
+            assert rel_l2(got[t], ref[t]) < 1e-5, t
+        assert np.array_equal(_bits(y), oracle.encode_act(got, BF16, "rne"))
+        _decode_paths_agree(gpu, layer, x, ids, wts, yf)
     finally:
         _free(layer, experts, sh)
 
@@ -686,8 +705,8 @@ def test_config4_node_share_layer_matches_oracle(gpu, oracle):
     """One layer of the config-4 node share: 64 resident experts of 256 (e = 0
     mod 4), no shared expert, 32 tokens routed under the resident mask with a
     Zipf-skewed bias (the grouped path).  Routes against the oracle's masked
-    router; a token sample against the oracle; every token against the
-    decode pipeline."""
+    router; every token's output against the oracle fed the device-resident
+    weights, and against the decode pipeline."""
     print("[moe] config-4 node-share layer", flush=True)
     E, H, T = 256, 7168, 32
     from constellation_amd.engine import Expert, Layer
@@ -706,14 +725,15 @@ def test_config4_node_share_layer_matches_oracle(gpu, oracle):
         for t, (oi, ow, margins, _) in enumerate(_oracle_route(oracle, x, w, bias, resident=res)):
             if min(margins) > 1e-12:
                 assert idn[t][:len(oi)].tolist() == oi.tolist(), t
-        sample = _sample_tokens(idn, T)
-        used = sorted(set(idn[sample].ravel().tolist()) - {-1})
-        cpu = {e: oracle.gen_expert(87, 0x7000 + 4 * e) for e in used}
-        ref = _oracle_moe(oracle, [cpu.get(e) for e in range(E)], None,
-                          x.float().cpu().numpy()[sample], idn[sample], wn[sample])
-        got = yf.cpu().numpy()[sample]
-        assert rel_l2(got, ref) < 1e-5 and np.abs(got - ref).max() < 2e-2
-        _decode_paths_agree(gpu, layer, x, ids, wts, yf)  # all 32 tokens
+        hot = int(np.bincount(idn[idn >= 0]).argmax())
+        _downloaded_equals_generated(oracle, experts[hot], 87, 0x7000 + 4 * hot)
+        ref = _oracle_moe_all_tokens(oracle, experts, None, x.float().cpu().numpy(), idn, wn)
+        got = yf.cpu().numpy()
+        assert rel_l2(got, ref) < 1e-5 and np.abs(got - ref).max() < 2e-2  # all 32 tokens
+        for t in range(T):
+            assert rel_l2(got[t], ref[t]) < 1e-5, t
+        assert np.array_equal(_bits(y), oracle.encode_act(got, BF16, "rne"))
+        _decode_paths_agree(gpu, layer, x, ids, wts, yf)
     finally:
         torch.cuda.synchronize()
         layer.close()

@@ -122,11 +122,59 @@ def test_static_rejects_oversize(gpu):
     e = Expert.generate(0, 80, 0x580)
     try:
         x = gpu.gen_normal(80, 1, (33, 7168), 1.0, torch.bfloat16)
-        rc, _, _ = _run_static(e, x[:32].contiguous(), BF16)
+        # exactly at the limit: 32 tokens x inter 2048 fill the array (h_lo
+        # ends on its last byte); the output must still equal the context path
+        x32 = x[:32].contiguous()
+        rc, y1, yf1 = _run_static(e, x32, BF16)
         assert rc == CX_OK
+        y0, yf0 = _run_ctx(gpu, e, x32, BF16)
+        torch.cuda.synchronize()
+        assert torch.equal(yf0, yf1) and torch.equal(y0.view(torch.int16), y1.view(torch.int16))
         rc, _, _ = _run_static(e, x, BF16)
         assert rc == CX_EINVAL
         assert b"static" in lib().cx_last_error()
         torch.cuda.synchronize()
     finally:
+        e.free()
+
+
+@pytest.mark.parametrize("T", [1, 8])
+def test_static_under_graph_capture(gpu, T):
+    """One cx_expert_run_static call captured into a HIP graph (kernel
+    launches only: the first, eager call has looked up the static array),
+    replayed three times on new inputs with eager work and syncs between the
+    replays; every replay equals cx_expert_run bit for bit.  T = 1 takes the
+    k-part path, T = 8 the tile path."""
+    from constellation_amd._lib import CX_OK
+    from constellation_amd.engine import Expert
+    print(f"[no_alloc] graph capture T={T}", flush=True)
+    e = Expert.generate(0, 81, 0x5C0)
+    try:
+        xs = [gpu.gen_normal(81, 0x600 + i, (T, 7168), 1.0, torch.bfloat16) for i in range(4)]
+        x = xs[0].clone()
+        rc, y, yf = _run_static(e, x, BF16)  # eager warm-up on the same buffers
+        assert rc == CX_OK
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side, capture_error_mode="thread_local"):
+                from constellation_amd._lib import lib
+                from constellation_amd.engine import cx_dtype
+                rc = lib().cx_expert_run_static(0, C.byref(e.desc), x.data_ptr(), cx_dtype(x.dtype),
+                                                T, y.data_ptr(), BF16, yf.data_ptr(),
+                                                side.cuda_stream)
+        assert rc == CX_OK
+        for i in range(1, 4):
+            x.copy_(xs[i])
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            y0, yf0 = _run_ctx(gpu, e, xs[i], BF16)
+            torch.cuda.synchronize()
+            assert torch.equal(yf0, yf), i
+            assert torch.equal(y0.view(torch.int16), y.view(torch.int16)), i
+        del g
+    finally:
+        torch.cuda.synchronize()
         e.free()
