@@ -760,6 +760,189 @@ __global__ __launch_bounds__(64 * NW) void k_rate_valu(int iters, unsigned long 
     sink[blockIdx.x * 64 * NW + tid] = __float_as_uint(sum) ^ x;
 }
 
+// ---------------------------------------------------------------------------
+// Config 0 (one expert, one token) as one launch split over the inter
+// dimension, against the library's two launches (k_gate_up_kpart +
+// k_down_ks).  Workgroup b owns inter rows [8b, 8b + 8): it issues its gate
+// and up rows (8 + 8 MFMA rows x 7168, K over 8 waves) and its down k-panel
+// (w_down stored as 8-column panels [I/8][H][8], 7168 rows x 8 B, 56 KB
+// contiguous) at once, forms h for its 8 rows in LDS, and writes the partial
+// y_b = Wd[:, 8b:8b+8] . h_b for all 7168 rows (fp32); a second launch sums
+// the 256 partials of each row in a fixed order.  FUSED_REDUCE = 0 times the
+// first launch alone.  The w_down bytes are the pool's synthetic bytes read
+// as panels (a re-layout would move them, not change the read pattern).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+constexpr int kF1Rows = 8;
+constexpr int kF1Wg = kI / kF1Rows;  // 256
+
+__global__ __launch_bounds__(512) void k_f1_expert(cx_expert_desc e, const uint16_t* x, float* ypart) {
+    constexpr int NKW = 7;  // k-blocks per wave (56 / 8)
+    __shared__ float red[8][16];
+    __shared__ float hs[kF1Rows];
+    typedef Mma<false> M;
+    const int b = blockIdx.x, wave = wave_id(), lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+    const int r0 = b * kF1Rows;
+    const uint8_t* pa = (c < 8 ? e.w_gate + (size_t)(r0 + c) * kH : e.w_up + (size_t)(r0 + c - 8) * kH) +
+                        (size_t)wave * NKW * kKB + g * 32;
+    u32x4 wa[NKW][2];
+#pragma unroll
+    for (int k = 0; k < NKW; ++k) {
+        wa[k][0] = ld16(pa + k * kKB);
+        wa[k][1] = ld16(pa + k * kKB + 16);
+    }
+    // down panel: this wave's 896 rows x 8 B, 16 B (two rows) per lane and load
+    const uint8_t* pp = e.w_down + (size_t)b * kH * 8 + (size_t)wave * 896 * 8 + lane * 16;
+    u32x4 wd[7];
+#pragma unroll
+    for (int j = 0; j < 7; ++j) wd[j] = ld16(pp + j * 1024);
+    // x (column 0 of B): 32 contiguous bf16 per lane and k-block, zero elsewhere
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, kH * 2);
+    u32x4 xb[NKW][4];
+#pragma unroll
+    for (int k = 0; k < NKW; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            xb[k][j] = bld16(xr, c == 0 ? (uint32_t)(((wave * NKW + k) * kKB + 32 * g + 8 * j) * 2) : kOob);
+    __builtin_amdgcn_sched_barrier(0);
+    const int rb = r0 / 128;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < NKW; ++k) {
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        f32x4 t = M::mma(M::cvt(wa[k][0][0], wa[k][0][1]), M::bits(xb[k][0]), zero);
+        t = M::mma(M::cvt(wa[k][0][2], wa[k][0][3]), M::bits(xb[k][1]), t);
+        t = M::mma(M::cvt(wa[k][1][0], wa[k][1][1]), M::bits(xb[k][2]), t);
+        t = M::mma(M::cvt(wa[k][1][2], wa[k][1][3]), M::bits(xb[k][3]), t);
+        const int kb = wave * NKW + k;
+        const float sc = g < 2 ? ldsc(e.s_gate + rb * 56 + kb) : ldsc(e.s_up + rb * 56 + kb);
+        acc += sc * t;
+    }
+    if (c == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[wave][4 * g + i] = acc[i];
+    }
+    __syncthreads();
+    if (wave == 0 && lane < kF1Rows) {
+        float gs = 0.f, us = 0.f;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            gs += red[w][lane];
+            us += red[w][8 + lane];
+        }
+        hs[lane] = (gs / (1.0f + expf(-gs))) * us;
+    }
+    __syncthreads();
+    float h[kF1Rows];
+#pragma unroll
+    for (int i = 0; i < kF1Rows; ++i) h[i] = hs[i];
+    const int kbd = r0 / 128;  // the slice's column block of w_down's scales
+#pragma unroll
+    for (int j = 0; j < 7; ++j) {
+        const int R = wave * 896 + j * 128 + 2 * lane;
+        const float sd = ldsc(e.s_down + (size_t)(wave * 7 + j) * 16 + kbd);
+        float y2[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint32_t w0 = wd[j][2 * q], w1 = wd[j][2 * q + 1];
+            const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w0, false);
+            const f32x2 bq = __builtin_amdgcn_cvt_pk_f32_fp8(w0, true);
+            const f32x2 cq = __builtin_amdgcn_cvt_pk_f32_fp8(w1, false);
+            const f32x2 dq = __builtin_amdgcn_cvt_pk_f32_fp8(w1, true);
+            float sum = a[0] * h[0];
+            sum += a[1] * h[1];
+            sum += bq[0] * h[2];
+            sum += bq[1] * h[3];
+            sum += cq[0] * h[4];
+            sum += cq[1] * h[5];
+            sum += dq[0] * h[6];
+            sum += dq[1] * h[7];
+            y2[q] = sum * sd;
+        }
+        *reinterpret_cast<float2*>(ypart + (size_t)b * kH + R) = float2{y2[0], y2[1]};
+    }
+}
+
+// y[r] = sum over the 256 partials in a fixed order: 16 groups of 16
+// consecutive partials per thread, then the 16 group sums in group order.
+__global__ __launch_bounds__(256) void k_f1_reduce(const float* ypart, uint16_t* y) {
+    __shared__ float4 red[16][16];
+    const int c4 = threadIdx.x & 15, grp = threadIdx.x >> 4;
+    const int row = blockIdx.x * 64 + c4 * 4;
+    float4 v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = *reinterpret_cast<const float4*>(ypart + (size_t)(grp * 16 + i) * kH + row);
+    float4 s = v[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) s = float4{s.x + v[i].x, s.y + v[i].y, s.z + v[i].z, s.w + v[i].w};
+    red[grp][c4] = s;
+    __syncthreads();
+    if (grp == 0) {
+        float4 t = red[0][c4];
+        for (int i = 1; i < 16; ++i) t = float4{t.x + red[i][c4].x, t.y + red[i][c4].y, t.z + red[i][c4].z, t.w + red[i][c4].w};
+        const f32x4 tv = {t.x, t.y, t.z, t.w};
+        store_out4(y, nullptr, (size_t)row, tv, CX_DTYPE_BF16);
+    }
+}
+
+int cmd_fused1(int iters) {
+    Pool pool(true);
+    std::printf("fused1: one expert, one token, 64 experts rotated (24 x 2 GiB chunks)\n");
+    const int lds = max_lds();
+    uint16_t *x = nullptr, *y = nullptr;
+    float *gu = nullptr, *yp = nullptr;
+    KB_CHECK(hipMalloc(&x, kH * 2));
+    KB_CHECK(hipMemset(x, 0x3c, kH * 2));
+    KB_CHECK(hipMalloc(&y, kH * 2));
+    KB_CHECK(hipMalloc(&gu, 2 * 2 * kI * 4));
+    KB_CHECK(hipMalloc(&yp, (size_t)kF1Wg * kH * 4));
+    const int n = std::min<int>(64, (int)pool.d.size());
+    auto two = [&](int i) {
+        ExpertLaunch L{};
+        L.single = pool.d[(i * 17) % pool.d.size()];
+        L.n_tokens = 1;
+        L.hidden = kH;
+        L.inter = kI;
+        L.maxt = 1;
+        L.x = x;
+        L.in_dtype = CX_DTYPE_BF16;
+        L.y = y;
+        L.out_dtype = CX_DTYPE_BF16;
+        L.np_lds = 1;
+        L.max_lds = lds;
+        L.gu_part = gu;
+        L.gu_kparts = 2;
+        return L;
+    };
+    const double bytes = 3.0 * kMat + 3 * 16 * 56 * 4 + 2 * kH * 2;
+    for (int rep = 0; rep < 3; ++rep) {
+        report("two launches: k_gate_up_kpart + k_down_ks", time_launches(iters, [&](int i) {
+                   const ExpertLaunch L = two(i % n);
+                   KB_CHECK(launch_gate_up_kpart(L, 0));
+                   KB_CHECK(launch_down_ks(L, 0));
+               }), bytes);
+        report("  k_gate_up_kpart alone", time_launches(iters, [&](int i) {
+                   KB_CHECK(launch_gate_up_kpart(two(i % n), 0));
+               }), bytes * 2 / 3);
+        report("split over inter: k_f1_expert + k_f1_reduce", time_launches(iters, [&](int i) {
+                   const cx_expert_desc& e = pool.d[((i % n) * 17) % pool.d.size()];
+                   cx_launch(k_f1_expert, dim3(kF1Wg), dim3(512), 0, (hipStream_t)0, e, (const uint16_t*)x, yp);
+                   cx_launch(k_f1_reduce, dim3(kH / 64), dim3(256), 0, (hipStream_t)0, (const float*)yp, y);
+               }), bytes);
+        report("  k_f1_expert alone", time_launches(iters, [&](int i) {
+                   const cx_expert_desc& e = pool.d[((i % n) * 17) % pool.d.size()];
+                   cx_launch(k_f1_expert, dim3(kF1Wg), dim3(512), 0, (hipStream_t)0, e, (const uint16_t*)x, yp);
+               }), bytes);
+        report("  k_f1_reduce alone", time_launches(iters, [&](int) {
+                   cx_launch(k_f1_reduce, dim3(kH / 64), dim3(256), 0, (hipStream_t)0, (const float*)yp, y);
+               }), (double)kF1Wg * kH * 4);
+    }
+    (void)hipFree(x);
+    (void)hipFree(y);
+    (void)hipFree(gu);
+    (void)hipFree(yp);
+    return 0;
+}
+
 int cmd_rates(int iters) {
     const int cus = n_cu();
     const int n = 2000 * std::max(1, iters / 30);
@@ -827,6 +1010,7 @@ int main(int argc, char** argv) {
     if (!std::strcmp(cmd, "decode-balance")) return cmd_decode_balance(iters);
     if (!std::strcmp(cmd, "grouped")) return cmd_grouped(std::min(iters, 12));
     if (!std::strcmp(cmd, "rates")) return cmd_rates(iters);
-    std::fprintf(stderr, "usage: cx_kbench layout|decode-down|placement|decode-balance|grouped|rates [launches]\n");
+    if (!std::strcmp(cmd, "fused1")) return cmd_fused1(iters);
+    std::fprintf(stderr, "usage: cx_kbench layout|decode-down|placement|decode-balance|grouped|rates|fused1 [launches]\n");
     return 2;
 }
