@@ -97,17 +97,17 @@ inline size_t gate_up_lds_bytes(int ksa, int maxt, int np_lds, int hidden) {
 // sums to L.gu_part[kpart][gate, up][token][row] instead of h; the parts are
 // summed in order and SiLU'd later (shared_h_finalize), so a small grid can
 // spread one expert's rows over twice the CUs.
+// gate_up_tile_unit: the tile of a work unit the caller has resolved (u.np
+// > 0); gate_up_tile resolves it from the launch first.
 template <int NKB, int D, int MAXT, bool F16, bool XLDS, int KS, bool SINGLE, int KSA = KS,
           int TR = kTileRows, bool PARTIAL = false>
-__device__ __forceinline__ void gate_up_tile(const ExpertLaunch& L, int tile, int item,
-                                             unsigned char* lds, int kpart = 0) {
+__device__ __forceinline__ void gate_up_tile_unit(const ExpertLaunch& L, int tile, const Unit& u,
+                                                  unsigned char* lds, int kpart = 0) {
     static_assert(!PARTIAL || (SINGLE && MAXT == 1), "k-part sums: single mode, <= 16 tokens");
     typedef Mma<F16> M;
     typedef typename M::V V;
     f32x4* red = reinterpret_cast<f32x4*>(lds);  // [KSA][MAXT][2][64]
     unsigned char* xlds = lds + gate_up_red_bytes(KSA, MAXT);
-    Unit u;
-    if (!resolve_unit<SINGLE>(L, item, kTileTok * MAXT, &u)) return;
     const int H = u.e.hidden, I = u.e.inter;
     static_assert(TR == 16 || TR == 8, "tile rows");
     const int r0 = tile * TR;
@@ -296,6 +296,15 @@ __device__ __forceinline__ void gate_up_tile(const ExpertLaunch& L, int tile, in
                 *reinterpret_cast<float4*>(L.h_f32 + p * I + row) = float4{hv[0], hv[1], hv[2], hv[3]};
         }
     }
+}
+
+template <int NKB, int D, int MAXT, bool F16, bool XLDS, int KS, bool SINGLE, int KSA = KS,
+          int TR = kTileRows, bool PARTIAL = false>
+__device__ __forceinline__ void gate_up_tile(const ExpertLaunch& L, int tile, int item,
+                                             unsigned char* lds, int kpart = 0) {
+    Unit u;
+    if (!resolve_unit<SINGLE>(L, item, kTileTok * MAXT, &u)) return;
+    gate_up_tile_unit<NKB, D, MAXT, F16, XLDS, KS, SINGLE, KSA, TR, PARTIAL>(L, tile, u, lds, kpart);
 }
 
 

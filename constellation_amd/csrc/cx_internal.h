@@ -247,6 +247,18 @@ hipError_t launch_dec_plan_sgu(const int32_t* ids, const float* w, int n_tokens,
                                PlanPtrs plan, int* err_flag, const ExpertLaunch* sg,
                                hipStream_t s);
 
+// One-token decode with the selection inside the routed gate/up launch (no
+// resident mask, every expert of the table resident, 256 experts in 8
+// groups, at most 8 picks, bf16 x, x staged in LDS): stage 1 = router
+// logits and scores (sc: s [E] then c [E], fp64) beside the
+// shared expert's gate/up k-parts (sg nullable; else its gu_part with 2
+// k-parts); stage 2 = the routed gate/up, each workgroup selecting for
+// itself, writing the routes (R.ids / R.wout) and the one-token plan for
+// launch_down_comb1, and finalising the shared h (L.gu_part).
+bool dec_fused_sel_ok(int n_experts, int n_group, int topk_group, int hidden, int top_k, int x_dtype);
+hipError_t launch_dec_logits_sgu(const RouteArgs& r, const ExpertLaunch* sg, double* sc, hipStream_t s);
+hipError_t launch_gate_up_sel(const ExpertLaunch& L, const RouteArgs& r, const double* sc, hipStream_t s);
+
 // Upload helpers / generator.
 hipError_t launch_canonicalize_fp8(uint8_t* p, uint64_t n, hipStream_t s);
 hipError_t launch_gen_fp8(uint64_t seed, uint64_t stream_id, int rows, int cols, int rb,

@@ -1429,6 +1429,222 @@ __global__ __launch_bounds__(NTHR) void k_dec_select_sgu(FusedArgs A, ExpertLaun
     dec_plan_core(S, T, K, E, A.has_shared, A.plan, A.err_flag, 0);
 }
 
+// ---------------------------------------------------------------------------
+// One-token decode with the selection inside the routed gate/up launch.
+// The two-stage router (logits; selection + planner beside the shared gate/up)
+// becomes: stage 1 = logits and scores beside the shared gate/up; stage 2 =
+// the routed gate/up, in which every workgroup selects the token's experts
+// itself.  A workgroup of the routed gate/up already waits two dependent
+// memory round trips for its plan record before its first weight load; here
+// it waits for the scores and its expert's descriptor instead, plus the
+// selection's arithmetic, and the stage between them is gone.
+
+// Stage 1.  Blocks [0, E): router row e's logit (exact fp64 products and a
+// fixed-order sum, row_logits4) and its scores, s = sigmoid(logit) and
+// c = s + bias (expert_scores, fp64), into sc[e] and sc[E + e].  Blocks E..:
+// the shared expert's gate/up tiles as two k-parts (the split tiles of
+// k_dec_select_sgu), finalised by stage 2.  8-wave blocks.
+template <bool WF32, int NKB, int KSA, bool XLDS>
+__global__ __launch_bounds__(512) void k_dec_logits_sgu(FusedArgs A, ExpertLaunch SG, double* sc) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char dlds[];
+    const int E = A.n_experts;
+    if ((int)blockIdx.x >= E) {
+        constexpr int D = NKB < (XLDS ? 4 : 2) ? NKB : (XLDS ? 4 : 2);
+        const int b = blockIdx.x - E;
+        gate_up_tile<NKB, D, 1, false, XLDS, 8, true, KSA, kTileRows, true>(SG, b / 2, 0, dlds, b % 2);
+        return;
+    }
+    const int e = blockIdx.x;
+    row_logits4<WF32, 512>(A.x, A.w, e, 0, 1, A.hidden, E, A.logits, reinterpret_cast<double*>(dlds));
+    if (threadIdx.x == 0) {  // the thread that stored the logit
+        double sv, cv;
+        expert_scores(A.logits[e], A.bias[e], true, &sv, &cv);
+        sc[e] = sv;
+        sc[E + e] = cv;
+    }
+}
+
+// Selection of one token specialised to 256 experts in 8 groups of 32 (the
+// DeepSeek-V3 router) and at most 8 picks, branch-free, for the one-token
+// fused path.  Lane l holds the choice scores c of experts 4l..4l+3 (group
+// l/8).  The decisions are select_reg's: a group's score is the sum of its
+// two largest c (a sum over a multiset, so ties cannot change it); groups
+// rank by score, then lower index; each pick is the largest remaining c,
+// ties to the lower expert index (the lowest lane holding it, then its
+// lowest slot).  Returns the picks' ids, wave-uniform.
+constexpr int kSel256Experts = 256, kSel256Groups = 8, kSel256MaxPicks = 8;
+
+struct Picks8 {
+    int id[kSel256MaxPicks];
+};
+
+__device__ __forceinline__ double max_d(double a, double b) { return a > b ? a : b; }
+__device__ __forceinline__ double min_d(double a, double b) { return a < b ? a : b; }
+
+// (a, b) = the two largest of this lane's and lane CTRL's pairs
+template <int CTRL>
+__device__ __forceinline__ void top2_with(double& a, double& b) {
+    const double oa = dpp_d<CTRL, 0xF, 0xF>(a), ob = dpp_d<CTRL, 0xF, 0xF>(b);
+    const double na = max_d(a, oa);
+    b = max_d(min_d(a, oa), max_d(b, ob));
+    a = na;
+}
+
+// Group stage: keeps the topk_group best groups' scores and sets the
+// others' to -inf.
+__device__ __forceinline__ void groups256(double c[4], int topk_group) {
+    const int lane = threadIdx.x & 63;
+    // the group's two largest: this lane's four, then across its 8 lanes
+    // (quad_perm [1,0,3,2], [2,3,0,1], then row_half_mirror: i <-> 7 - i)
+    const double m01 = max_d(c[0], c[1]), n01 = min_d(c[0], c[1]);
+    const double m23 = max_d(c[2], c[3]), n23 = min_d(c[2], c[3]);
+    double a = max_d(m01, m23), b = max_d(min_d(m01, m23), max_d(n01, n23));
+    top2_with<0xB1>(a, b);
+    top2_with<0x4E>(a, b);
+    top2_with<0x141>(a, b);
+    const double gs = a + b;
+    const int myg = lane >> 3;
+    int grank = 0;
+#pragma unroll
+    for (int g = 0; g < kSel256Groups; ++g) {
+        const double o = readlane_d(gs, 8 * g);
+        grank += (o > gs || (o == gs && g < myg)) ? 1 : 0;
+    }
+    const bool keep = grank < topk_group;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = keep ? c[i] : -INFINITY;
+}
+
+// Pick stage: the top_k largest remaining scores, in order.
+__device__ __forceinline__ Picks8 picks256(double c[4], int top_k) {
+    const int lane = threadIdx.x & 63;
+    Picks8 p;
+#pragma unroll
+    for (int r = 0; r < kSel256MaxPicks; ++r) {
+        p.id[r] = -1;
+        if (r < top_k) {
+            double m = max_d(max_d(c[0], c[1]), max_d(c[2], c[3]));
+            m = max_d(m, dpp_d<0x111, 0xF, 0xF>(m));
+            m = max_d(m, dpp_d<0x112, 0xF, 0xF>(m));
+            m = max_d(m, dpp_d<0x114, 0xF, 0xF>(m));
+            m = max_d(m, dpp_d<0x118, 0xF, 0xF>(m));
+            m = max_d(m, dpp_d<0x142, 0xA, 0xF>(m));
+            m = max_d(m, dpp_d<0x143, 0xC, 0xF>(m));
+            const double M = readlane_d(m, 63);
+            const int fs = c[0] == M ? 0 : c[1] == M ? 1 : c[2] == M ? 2 : c[3] == M ? 3 : 4;
+            const unsigned long long hit = __ballot(fs < 4);
+            const int owner = static_cast<int>(__builtin_ctzll(hit));
+            const int slot = __builtin_amdgcn_readlane(fs, owner);
+            p.id[r] = owner * 4 + slot;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) c[i] = (lane == owner && i == slot) ? -INFINITY : c[i];
+        }
+    }
+    return p;
+}
+
+struct SelArgs {
+    const double* sc;  // s [E] then c [E] of stage 1
+    int n_experts, n_group, topk_group, top_k, norm, has_shared;
+    float scale;
+    int32_t* ids;      // [top_k] routes out (descending choice score)
+    float* wout;       // [top_k]
+};
+
+// The routes (weights as select_reg forms them: s of the picks normalised
+// by their sum in pick order, + 1e-20, then scaled) and the one-token plan
+// the down + combine launch reads (down_comb1_tile): routed item i = the
+// pick with the i-th smallest expert id (the planner's slot order) owns
+// pair s0 + i, the shared expert pair 0; token_pairs[k] = pair of route k
+// (column top_k: the shared pair).  Lane r < top_k holds pick r and its id
+// rank.
+__device__ __forceinline__ void dec_sel_plan(const ExpertLaunch& L, const SelArgs& S, int isel,
+                                             int rank, int s0) {
+    const int lane = threadIdx.x & 63, K = S.top_k;
+    const double sv = lane < K ? S.sc[isel] : 0.0;
+    double wsum = 0.0;
+    for (int r = 0; r < K; ++r) wsum += readlane_d(sv, r);
+    double v = sv;
+    if (S.norm && K > 1) v /= wsum + 1e-20;
+    v *= static_cast<double>(S.scale);
+    if (lane < K) {
+        S.ids[lane] = isel;
+        S.wout[lane] = static_cast<float>(v);
+        L.plan.token_pairs[lane] = s0 + rank;
+    }
+    if (lane == K) L.plan.token_pairs[K] = s0 ? 0 : -1;
+    if (lane < K || (s0 && lane == K)) {
+        const bool routed = lane < K;
+        const cx_expert_desc d = L.table[routed ? isel : S.n_experts];  // entry E: the shared expert
+        L.plan.item_rec[routed ? rank : K] =
+            ItemRec{d.w_up, d.w_gate, d.w_down, d.s_up, d.s_gate, d.s_down, routed ? s0 + rank : 0, 1,
+                    d.up_rb, d.gate_rb, d.down_rb, 0, {0, 0, 0, 0}};
+    }
+    if (lane == 0) {
+        PlanHdr h{};
+        h.n_slots = h.n_items = h.n_pairs = K + s0;
+        h.n_routed_slots = h.n_routed_items = K;
+        *L.plan.hdr = h;
+    }
+}
+
+// Stage 2: grid (inter / 16 row tiles, top_k picks [+ 1]).  Wave 0 of every
+// workgroup selects (select256 on stage 1's choice scores: the same inputs
+// and code everywhere, so every workgroup finds the same picks), numbers the
+// picks by ascending expert id and hands pick blockIdx.y's expert to the
+// other waves through LDS; the workgroup then streams row tile blockIdx.x of
+// that expert's gate and up (gate_up_tile_unit, x staged in LDS).  With a
+// shared expert, the last grid row finalises its h from stage 1's k-part
+// sums.
+template <int NKB>
+__global__ __launch_bounds__(256) void k_gate_up_sel(ExpertLaunch L, SelArgs S) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char gu_lds[];
+    if (L.gu_part != nullptr && blockIdx.y == gridDim.y - 1) {
+        shared_h_finalize(L, blockIdx.x);
+        return;
+    }
+    __shared__ int s_expert;  // this workgroup's expert, or -1
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int item = blockIdx.y, K = S.top_k;
+    const int s0 = S.has_shared ? 1 : 0;
+    if (wave == 0) {
+        double c[4];
+        {
+            const u32x4 v0 = ld16(S.sc + kSel256Experts + 4 * lane);
+            const u32x4 v1 = ld16(S.sc + kSel256Experts + 4 * lane + 2);
+            c[0] = __longlong_as_double((static_cast<long long>(v0[1]) << 32) | v0[0]);
+            c[1] = __longlong_as_double((static_cast<long long>(v0[3]) << 32) | v0[2]);
+            c[2] = __longlong_as_double((static_cast<long long>(v1[1]) << 32) | v1[0]);
+            c[3] = __longlong_as_double((static_cast<long long>(v1[3]) << 32) | v1[2]);
+        }
+        groups256(c, S.topk_group);
+        const Picks8 p = picks256(c, K);
+        int isel = -1;  // lane r < K: pick r
+#pragma unroll
+        for (int r = 0; r < kSel256MaxPicks; ++r) isel = lane == r ? p.id[r] : isel;
+        int rank = 0;  // of this lane's pick among the picks, by expert id
+#pragma unroll
+        for (int r = 0; r < kSel256MaxPicks; ++r) rank += (r < K && p.id[r] < isel) ? 1 : 0;
+        const unsigned long long hit = __ballot(lane < K && rank == item);
+        if (lane == 0)
+            s_expert = item < K ? __builtin_amdgcn_readlane(isel, static_cast<int>(__builtin_ctzll(hit))) : -1;
+        if (blockIdx.x == 0 && item == 0) dec_sel_plan(L, S, isel, rank, s0);
+    }
+    __syncthreads();
+    const int e = __builtin_amdgcn_readfirstlane(s_expert);
+    if (e < 0) return;
+    Unit u;
+    u.e = ld_uniform(L.table + e);
+    u.e.hidden = L.hidden;
+    u.e.inter = L.inter;
+    u.pb = s0 + item;
+    u.np = 1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) u.tok[q] = 0;
+    constexpr int D = NKB < 4 ? NKB : 4;
+    gate_up_tile_unit<NKB, D, 1, false, true, 4, false>(L, blockIdx.x, u, gu_lds);
+}
+
 // Decode stage 1' (routes given): workgroup 0 validates the routes (range,
 // repeats within a token: validate_routes, server/moe_layer_runtime.py:84-98)
 // and builds the plan; blocks 1.. run the shared expert's gate/up tiles.
@@ -1634,6 +1850,51 @@ hipError_t launch_dec_plan_sgu(const int32_t* ids, const float* w, int n_tokens,
         case 4: go_dec_plan<1>(P, sg, s); break;
         default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+bool dec_fused_sel_ok(int n_experts, int n_group, int topk_group, int hidden, int top_k, int x_dtype) {
+    const int nkb = hidden / kKB;
+    return n_experts == kSel256Experts && n_group == kSel256Groups && topk_group >= 1 &&
+           topk_group <= kSel256Groups && top_k >= 1 && top_k <= kSel256MaxPicks &&
+           hidden % 512 == 0 && (nkb == 56 || nkb == 8) && x_dtype == CX_DTYPE_BF16;
+}
+
+hipError_t launch_dec_logits_sgu(const RouteArgs& R, const ExpertLaunch* sg, double* sc, hipStream_t s) {
+    if (R.n_tokens != 1 || R.resident != nullptr || sc == nullptr ||
+        !dec_fused_sel_ok(R.n_experts, R.n_group, R.topk_group, R.hidden, R.top_k, R.x_dtype))
+        return hipErrorInvalidValue;
+    if (sg != nullptr && (sg->gu_part == nullptr || sg->gu_kparts != 2)) return hipErrorInvalidValue;
+    const FusedArgs A = fused_args(R);
+    ExpertLaunch none{};
+    const ExpertLaunch& G = sg ? *sg : none;
+    const bool xl = sg != nullptr && sg->np_lds > 0;
+    const bool big = R.hidden / kKB == 56;
+    const size_t lds = std::max<size_t>(8 * 4 * sizeof(double),
+                                        sg ? gate_up_lds_bytes(big ? 7 : 4, 1, xl ? sg->np_lds : 0, R.hidden) : 0);
+    const dim3 grid(R.n_experts + (sg ? 2 * (sg->inter / kTileRows) : 0)), block(512);
+    const bool wf = R.w_dtype == CX_DTYPE_F32;
+#define CX_GO(WF, NKB, KSA, XL) cx_launch((k_dec_logits_sgu<WF, NKB, KSA, XL>), grid, block, lds, s, A, G, sc)
+    if (big) {
+        if (wf) { if (xl) CX_GO(true, 4, 7, true); else CX_GO(true, 4, 7, false); }
+        else { if (xl) CX_GO(false, 4, 7, true); else CX_GO(false, 4, 7, false); }
+    } else {
+        if (wf) { if (xl) CX_GO(true, 1, 4, true); else CX_GO(true, 1, 4, false); }
+        else { if (xl) CX_GO(false, 1, 4, true); else CX_GO(false, 1, 4, false); }
+    }
+#undef CX_GO
+    return hipGetLastError();
+}
+
+hipError_t launch_gate_up_sel(const ExpertLaunch& L, const RouteArgs& R, const double* sc, hipStream_t s) {
+    if (L.table == nullptr || L.n_tokens != 1 || L.np_lds < 1 || L.maxt != 1 || sc == nullptr ||
+        !dec_fused_sel_ok(R.n_experts, R.n_group, R.topk_group, L.hidden, R.top_k, L.in_dtype))
+        return hipErrorInvalidValue;
+    SelArgs S{sc, R.n_experts, R.n_group, R.topk_group, R.top_k, R.norm, R.has_shared, R.scale, R.ids, R.wout};
+    const dim3 grid(L.inter / kTileRows, R.top_k + (L.gu_part != nullptr ? 1 : 0)), block(256);
+    const size_t lds = gate_up_lds_bytes(4, 1, L.np_lds, L.hidden);
+    if (L.hidden / kKB == 56) cx_launch((k_gate_up_sel<14>), grid, block, lds, s, L, S);
+    else cx_launch((k_gate_up_sel<2>), grid, block, lds, s, L, S);
     return hipGetLastError();
 }
 

@@ -233,6 +233,7 @@ struct cx_ctx {
     int n_cu = 0;                      // compute units (0: unknown)
     DevBuf plan_buf, hhi, hlo, ypart, logits, route_ids, route_w, hscratch;
     DevBuf gu_part;                    // shared expert's k-part gate/up sums (decode)
+    DevBuf scores;                     // one-token router scores s, c [E][2] fp64 (decode)
     int route_T = 0, route_E = 0;      // shape of the fp64 logits of the last router call
     DevBuf dx, dy;                     // cx_expert_run_host staging (device)
     void* pin_x = nullptr;             // pinned host staging
@@ -559,6 +560,24 @@ int moe_decode(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, 
         SG.gu_kparts = 2;
     }
     const int routed_items = std::min(T * top_k, layer->n_experts);
+    // One token with the router, no resident mask, every expert of the table
+    // resident and the one-launch down + combine: the selection runs inside
+    // the routed gate/up launch (each workgroup selects for itself), so the
+    // stage between the logits and the routed gate/up is gone; the shared
+    // expert's gate/up k-parts move beside the logits.
+    const bool fused = route != nullptr && T == 1 && route->resident == nullptr &&
+                       route->n_experts == layer->n_experts && route->top_k == top_k &&
+                       layer->n_resident == layer->n_experts && np_lds > 0 &&
+                       (sg == nullptr || split) &&
+                       down_comb1_ok(layer->hidden, layer->inter, top_k, ctx->max_lds) &&
+                       dec_fused_sel_ok(route->n_experts, route->n_group, route->topk_group,
+                                        layer->hidden, top_k, route->x_dtype);
+    double* sc = nullptr;
+    if (fused) {
+        int rc = ensure(&ctx->scores, sizeof(double) * 2 * (size_t)layer->n_experts, s);
+        if (rc) return rc;
+        sc = static_cast<double*>(ctx->scores.p);
+    }
     if (route != nullptr) {
         route->plan = &P;
         route->table = layer->table;
@@ -566,13 +585,18 @@ int moe_decode(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, 
         route->item_cap = z.item_cap;
         route->max_items = z.max_items;
         route->err_flag = ctx->err_flag;
-        {
+        if (fused) {
             Span sp(ctx, "route", s);
-            CX_HIP(launch_dec_logits(*route, s));
-        }
-        {
-            Span sp(ctx, "plan", s);
-            CX_HIP(launch_dec_select_sgu(*route, sg, s));
+            CX_HIP(launch_dec_logits_sgu(*route, sg, sc, s));
+        } else {
+            {
+                Span sp(ctx, "route", s);
+                CX_HIP(launch_dec_logits(*route, s));
+            }
+            {
+                Span sp(ctx, "plan", s);
+                CX_HIP(launch_dec_select_sgu(*route, sg, s));
+            }
         }
     } else {
         Span sp(ctx, "plan", s);
@@ -599,7 +623,10 @@ int moe_decode(cx_ctx* ctx, const cx_layer* layer, const void* x, int in_dtype, 
     L.skip_shared = 1;
     L.gu_part = SG.gu_part;
     L.gu_kparts = SG.gu_kparts;
-    if (L.max_items > 0 || L.gu_part != nullptr) {
+    if (fused) {
+        Span sp(ctx, "gate_up", s);
+        CX_HIP(launch_gate_up_sel(L, *route, sc, s));
+    } else if (L.max_items > 0 || L.gu_part != nullptr) {
         Span sp(ctx, "gate_up", s);
         CX_HIP(launch_gate_up(L, s));
     }
@@ -990,7 +1017,7 @@ int cx_ctx_destroy(cx_ctx* c) {
     (void)hipDeviceSynchronize();
     drain_spans(c);
     DevBuf* bufs[] = {&c->plan_buf, &c->hhi, &c->hlo, &c->ypart, &c->logits, &c->route_ids,
-                      &c->route_w, &c->hscratch, &c->gu_part, &c->dx, &c->dy};
+                      &c->route_w, &c->hscratch, &c->gu_part, &c->scores, &c->dx, &c->dy};
     for (DevBuf* b : bufs)
         if (b->p) (void)hipFree(b->p);
     if (c->err_flag) (void)hipFree(c->err_flag);

@@ -476,7 +476,8 @@ def test_one_token_down_combine(gpu, oracle, H, I, shared, K, dtype, odtype):
 
 
 @pytest.mark.parametrize("T,E,shared,wdtype,mask", [
-    (1, 64, True, torch.bfloat16, False), (2, 64, True, torch.bfloat16, False),
+    (1, 64, True, torch.bfloat16, False), (1, 128, True, torch.float32, False),
+    (1, 256, False, torch.bfloat16, False), (2, 64, True, torch.bfloat16, False),
     (5, 128, True, torch.float32, False), (16, 64, True, torch.bfloat16, False),
     (3, 256, False, torch.bfloat16, False), (4, 64, True, torch.bfloat16, True),
     (16, 256, True, torch.bfloat16, True)])
@@ -511,6 +512,55 @@ def test_moe_layer_decode_pipeline(gpu, oracle, T, E, shared, wdtype, mask):
         assert rel_l2(yf, ref) < 1e-5, rel_l2(yf, ref)
         assert np.abs(yf - ref).max() < 2e-2
         assert np.array_equal(_bits(y), oracle.encode_act(yf, BF16, "rne"))
+    finally:
+        _free(layer, experts, sh)
+
+
+@pytest.mark.parametrize("E,H,I,shared,TG,K", [(256, 1024, 512, True, 4, 8),
+                                               (256, 1024, 512, False, 3, 6),
+                                               (256, 7168, 2048, True, 4, 8)])
+def test_one_token_fused_selection_equals_staged(gpu, oracle, E, H, I, shared, TG, K):
+    """At one token without a resident mask, cx_moe_layer selects inside the
+    routed gate/up launch (every workgroup selects for itself).  A resident
+    mask of all ones selects the same experts through the staged pipeline
+    (selection + planner launch).  Both sum each router row's exact fp64
+    products, over 512 and 256 threads, so a logit can differ in its last
+    fp64 bit and a weight, rarely, by one fp32 ulp: routes must be equal,
+    weights within one ulp, and where the weights are equal (all but a
+    ~1e-9 chance) both outputs bit-identical.  Several tokens in turn (no
+    state carried between calls); the routes equal the oracle's."""
+    print(f"[moe] fused selection E={E} H={H} shared={shared} TG={TG} K={K}", flush=True)
+    if H == 7168:
+        from constellation_amd.engine import Expert, Layer
+        experts = [Expert.generate(0, 95, 0x5800 + 4 * e) for e in range(E)]
+        sh = Expert.generate(0, 95, 0x5800 + 4 * E) if shared else None
+        layer = Layer(gpu, experts, sh)
+    else:
+        layer, experts, sh, _, _ = _make_layer(gpu, oracle, E, H, I, seed=95, shared=shared)
+    try:
+        _, w, bias = _router_inputs(gpu, 96, 1, E, H)
+        ones = torch.ones(E, dtype=torch.uint8, device="cuda")
+        for i in range(4):
+            x = gpu.gen_normal(97 + i, 3, (1, H), 1.0, torch.bfloat16)
+            a = gpu.moe_layer(layer, x, w, bias, n_group=8, topk_group=TG, top_k=K, want_f32=True)
+            b = gpu.moe_layer(layer, x, w, bias, resident=ones, n_group=8, topk_group=TG, top_k=K,
+                              want_f32=True)
+            gpu.sync()
+            ya, yfa, ida, wa = (t.cpu() for t in a)
+            yb, yfb, idb, wb = (t.cpu() for t in b)
+            assert torch.equal(ida, idb), i
+            ulps = (wa.view(torch.int32).long() - wb.view(torch.int32).long()).abs()
+            assert int(ulps.max()) <= 1, i
+            if int(ulps.max()) == 0:
+                assert torch.equal(yfa.view(torch.int32), yfb.view(torch.int32)), i
+                assert torch.equal(ya.view(torch.int16), yb.view(torch.int16)), i
+            else:
+                assert rel_l2(yfa.numpy(), yfb.numpy()) < 1e-6, i
+            oi, ow, margins, _ = _oracle_route(oracle, x, w, bias, n_group=8, topk_group=TG,
+                                               top_k=K)[0]
+            if min(margins) > 1e-12:
+                assert ida[0].tolist() == oi.tolist(), i
+                assert np.allclose(wa[0].numpy(), ow, rtol=1e-6, atol=0), i
     finally:
         _free(layer, experts, sh)
 
