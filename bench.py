@@ -13,7 +13,7 @@ tokens, so no step finds its 400 MB of weights in the 256 MB MALL.
 
 Prints one JSON line.  `value` is microseconds per token at B=1 (lower is
 better); `extras` carries B=16 and per-kernel figures.
-The roofline object covers the dominant kernel (gate_up): algorithmic bytes
+The roofline object covers the dominant kernel (the routed gate/up): algorithmic bytes
 per launch / its average duration measured with HIP events on the launch
 stream (cx_ctx_profile), against 8 TB/s.  cpu_baseline times the reference's
 own CPU expert path (oracle/_ref, RunFusedUpGateCpuV2 + RunDownCpuV2 with the
@@ -63,12 +63,13 @@ def parse() -> argparse.Namespace:
     return ap.parse_args()
 
 
-TRAFFIC_FILE = "profiles/k_gate_up_decode_b1_pmc.txt"
+TRAFFIC_FILE = "profiles/moe_layer_decode_b1_pmc.txt"
 
 
 def measured_traffic():
-    """HBM bytes per k_gate_up launch at B=1 from the committed rocprofv3 --pmc
-    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor), or None."""
+    """HBM bytes per routed gate/up launch at B=1 from the committed rocprofv3
+    --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor),
+    or None."""
     import re
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_FILE)
     try:
@@ -583,7 +584,8 @@ def main() -> int:
     gu = prof1["gate_up"]
     gu_bytes = gate_up_bytes(1, u1)
     gu_gbs = gu_bytes / (gu["avg_us"] * 1e-6) / 1e9 if gu["avg_us"] else None
-    roofline = {"bound": "hbm", "kernel": "k_gate_up (B=1 decode)", "achieved": gu_gbs,
+    roofline = {"bound": "hbm", "kernel": "routed gate/up (B=1 decode: k_gate_up_sel, selection inside)",
+                "achieved": gu_gbs,
                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": (gu_gbs / HBM_PEAK_GBS) if gu_gbs else None,
                 "algorithmic_bytes_per_launch": gu_bytes, "traffic": measured_traffic(),

@@ -8,13 +8,16 @@
 //                          bare (no compute) in the natural row-major order and in
 //                          the tiled order a re-layout at upload would give
 //   cx_kbench decode-down  one-token down projection: k_down_comb1 (down + combine
-//                          in one launch) against k_down_item + k_combine_dec
+//                          in one launch) against k_down_item + k_combine_dec, and
+//                          the down bytes streamed bare, row-major and as k-panels
 //   cx_kbench placement    one-token gate/up and down launches with the experts
 //                          packed into one buffer vs spread over 24 x 2 GiB chunks
 //   cx_kbench decode-balance  one-token gate/up bytes streamed bare with tiles
 //                          handed out statically or claimed from per-XCD counters,
 //                          and k_down_comb1 over 256 / 384 / 448 / 512 tiles
 //   cx_kbench grouped      the grouped prefill kernels on the config-3-like plan
+//   cx_kbench fused1       one expert, one token: one launch split over inter (w_down
+//                          as k-panels) + a reduce launch, against the two launches
 //   cx_kbench rates        per-CU rates the LDS-ring kernels are built on, in shader
 //                          clocks (s_memtime): ds_read_b128 bytes per clock, bf16
 //                          MFMA and fp8 -> 16-bit convert issue intervals, and
@@ -250,16 +253,27 @@ __device__ __forceinline__ uint32_t fold(const u32x4 (&w)[2]) {
     return w[0][0] + w[0][1] * 3u + w[0][2] * 5u + w[0][3] * 7u + w[1][0] * 11u + w[1][1] * 13u + w[1][2] + w[1][3];
 }
 
+// KP: the matrices read as 32-column k-panels [I/32][H][32] (a lane's 32
+// bytes of row r, k-block k, quarter g at ((4k + g) * H + r) * 32) instead of
+// row-major [H][I] (at r * I + 128 k + 32 g): the same bytes per lane, 16
+// consecutive rows' 32-byte pieces contiguous instead of 16 rows 2 KB apart.
+template <bool KP>
+__device__ __forceinline__ size_t down_off(size_t r, int k, int g) {
+    return KP ? ((size_t)(4 * k + g) * kH + r) * 32 : r * kI + (size_t)k * kKB + g * 32;
+}
+
+template <bool KP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_bare_down_item(DownPtrs P, uint32_t* sink) {
     constexpr int NKB = 16, D = 6;
     const int wave = wave_id(), lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-    const uint8_t* p = P.m[blockIdx.y] + (size_t)(blockIdx.x * 64 + wave * 16 + c) * kI + g * 32;
+    const size_t r = (size_t)(blockIdx.x * 64 + wave * 16 + c);
+    const uint8_t* m = P.m[blockIdx.y];
     u32x4 wb[D][2];
     uint32_t acc = 0;
 #pragma unroll
     for (int s = 0; s < D; ++s) {
-        wb[s][0] = ld16(p + s * kKB);
-        wb[s][1] = ld16(p + s * kKB + 16);
+        wb[s][0] = ld16(m + down_off<KP>(r, s, g));
+        wb[s][1] = ld16(m + down_off<KP>(r, s, g) + 16);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -267,21 +281,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
         acc ^= fold(wb[k % D]);
         __builtin_amdgcn_sched_barrier(0);
         if (k + D < NKB) {
-            wb[k % D][0] = ld16(p + (k + D) * kKB);
-            wb[k % D][1] = ld16(p + (k + D) * kKB + 16);
+            wb[k % D][0] = ld16(m + down_off<KP>(r, k + D, g));
+            wb[k % D][1] = ld16(m + down_off<KP>(r, k + D, g) + 16);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
     if (acc == 0x12345678u) sink[threadIdx.x] = acc;
 }
 
+template <bool KP>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_bare_down_rows(DownPtrs P, uint32_t* sink) {
     constexpr int NK = 18, D = 8;
     const int wave = wave_id(), lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-    const size_t row = (size_t)(blockIdx.x * 16 + c) * kI;
-    const uint8_t* p = P.m[wave] + row + g * 32;
-    const uint8_t* q = P.m[8] + row + (size_t)(2 * wave) * kKB + g * 32;
-    auto at = [&](int k) { return k < 16 ? p + k * kKB : q + (k - 16) * kKB; };
+    const size_t r = (size_t)(blockIdx.x * 16 + c);
+    auto at = [&](int k) {
+        return k < 16 ? P.m[wave] + down_off<KP>(r, k, g) : P.m[8] + down_off<KP>(r, 2 * wave + k - 16, g);
+    };
     u32x4 wb[D][2];
     uint32_t acc = 0;
 #pragma unroll
@@ -321,11 +336,19 @@ int cmd_decode_down(int iters) {
         std::printf(" pass %d\n", rep + 1);
         report("bare stream, k_down_item shape (item x 64 rows)",
                time_launches(iters, [&](int i) {
-                   cx_launch(k_bare_down_item, dim3(112, 9), dim3(256), 0u, (hipStream_t)0, sets[i % 16], sink);
+                   cx_launch(k_bare_down_item<false>, dim3(112, 9), dim3(256), 0u, (hipStream_t)0, sets[i % 16], sink);
+               }), 9.0 * kMat);
+        report("  same bytes as 32-column k-panels",
+               time_launches(iters, [&](int i) {
+                   cx_launch(k_bare_down_item<true>, dim3(112, 9), dim3(256), 0u, (hipStream_t)0, sets[i % 16], sink);
                }), 9.0 * kMat);
         report("bare stream, k_down_comb1 shape (16 rows x all items)",
                time_launches(iters, [&](int i) {
-                   cx_launch(k_bare_down_rows, dim3(kH / 16), dim3(512), 0u, (hipStream_t)0, sets[i % 16], sink);
+                   cx_launch(k_bare_down_rows<false>, dim3(kH / 16), dim3(512), 0u, (hipStream_t)0, sets[i % 16], sink);
+               }), 9.0 * kMat);
+        report("  same bytes as 32-column k-panels",
+               time_launches(iters, [&](int i) {
+                   cx_launch(k_bare_down_rows<true>, dim3(kH / 16), dim3(512), 0u, (hipStream_t)0, sets[i % 16], sink);
                }), 9.0 * kMat);
         report("k_down_comb1 (down + combine)", time_launches(iters, [&](int i) {
                    ExpertLaunch L = dp.launch(i, table, lds);
