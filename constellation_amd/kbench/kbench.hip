@@ -253,16 +253,22 @@ __device__ __forceinline__ uint32_t fold(const u32x4 (&w)[2]) {
     return w[0][0] + w[0][1] * 3u + w[0][2] * 5u + w[0][3] * 7u + w[1][0] * 11u + w[1][1] * 13u + w[1][2] + w[1][3];
 }
 
-// KP: the matrices read as 32-column k-panels [I/32][H][32] (a lane's 32
-// bytes of row r, k-block k, quarter g at ((4k + g) * H + r) * 32) instead of
-// row-major [H][I] (at r * I + 128 k + 32 g): the same bytes per lane, 16
-// consecutive rows' 32-byte pieces contiguous instead of 16 rows 2 KB apart.
-template <bool KP>
-__device__ __forceinline__ size_t down_off(size_t r, int k, int g) {
-    return KP ? ((size_t)(4 * k + g) * kH + r) * 32 : r * kI + (size_t)k * kKB + g * 32;
+// KP: the layout the matrices are read in; the bytes each lane loads are
+// the same in all three (row r, k-block k, quarter g: 32 bytes as two
+// 16-byte pieces p = 0, 1):
+//   0  row-major [H][I]:               r * I + 128 k + 32 g + 16 p
+//   1  32-column k-panels [I/32][H][32]: ((4k + g) * H + r) * 32 + 16 p
+//      (a wave's 16 rows of one quarter are 512 contiguous bytes)
+//   2  16-column k-panels [I/16][H][16]: ((8k + 2g + p) * H + r) * 16
+//      (each 16-byte load instruction reads 8 whole 128-byte lines)
+template <int KP>
+__device__ __forceinline__ size_t down_off(size_t r, int k, int g, int p) {
+    if (KP == 1) return ((size_t)(4 * k + g) * kH + r) * 32 + 16 * p;
+    if (KP == 2) return ((size_t)(8 * k + 2 * g + p) * kH + r) * 16;
+    return r * kI + (size_t)k * kKB + g * 32 + 16 * p;
 }
 
-template <bool KP>
+template <int KP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_bare_down_item(DownPtrs P, uint32_t* sink) {
     constexpr int NKB = 16, D = 6;
     const int wave = wave_id(), lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
@@ -272,8 +278,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     uint32_t acc = 0;
 #pragma unroll
     for (int s = 0; s < D; ++s) {
-        wb[s][0] = ld16(m + down_off<KP>(r, s, g));
-        wb[s][1] = ld16(m + down_off<KP>(r, s, g) + 16);
+        wb[s][0] = ld16(m + down_off<KP>(r, s, g, 0));
+        wb[s][1] = ld16(m + down_off<KP>(r, s, g, 1));
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -281,28 +287,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
         acc ^= fold(wb[k % D]);
         __builtin_amdgcn_sched_barrier(0);
         if (k + D < NKB) {
-            wb[k % D][0] = ld16(m + down_off<KP>(r, k + D, g));
-            wb[k % D][1] = ld16(m + down_off<KP>(r, k + D, g) + 16);
+            wb[k % D][0] = ld16(m + down_off<KP>(r, k + D, g, 0));
+            wb[k % D][1] = ld16(m + down_off<KP>(r, k + D, g, 1));
         }
         __builtin_amdgcn_sched_barrier(0);
     }
     if (acc == 0x12345678u) sink[threadIdx.x] = acc;
 }
 
-template <bool KP>
+template <int KP>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_bare_down_rows(DownPtrs P, uint32_t* sink) {
     constexpr int NK = 18, D = 8;
     const int wave = wave_id(), lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
     const size_t r = (size_t)(blockIdx.x * 16 + c);
-    auto at = [&](int k) {
-        return k < 16 ? P.m[wave] + down_off<KP>(r, k, g) : P.m[8] + down_off<KP>(r, 2 * wave + k - 16, g);
+    auto at = [&](int k, int p) {
+        return k < 16 ? P.m[wave] + down_off<KP>(r, k, g, p) : P.m[8] + down_off<KP>(r, 2 * wave + k - 16, g, p);
     };
     u32x4 wb[D][2];
     uint32_t acc = 0;
 #pragma unroll
     for (int s = 0; s < D; ++s) {
-        wb[s][0] = ld16(at(s));
-        wb[s][1] = ld16(at(s) + 16);
+        wb[s][0] = ld16(at(s, 0));
+        wb[s][1] = ld16(at(s, 1));
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -310,8 +316,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
         acc ^= fold(wb[k % D]);
         __builtin_amdgcn_sched_barrier(0);
         if (k + D < NK) {
-            wb[k % D][0] = ld16(at(k + D));
-            wb[k % D][1] = ld16(at(k + D) + 16);
+            wb[k % D][0] = ld16(at(k + D, 0));
+            wb[k % D][1] = ld16(at(k + D, 1));
         }
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -336,19 +342,27 @@ int cmd_decode_down(int iters) {
         std::printf(" pass %d\n", rep + 1);
         report("bare stream, k_down_item shape (item x 64 rows)",
                time_launches(iters, [&](int i) {
-                   cx_launch(k_bare_down_item<false>, dim3(112, 9), dim3(256), 0u, (hipStream_t)0, sets[i % 16], sink);
+                   cx_launch(k_bare_down_item<0>, dim3(112, 9), dim3(256), 0u, (hipStream_t)0, sets[i % 16], sink);
                }), 9.0 * kMat);
         report("  same bytes as 32-column k-panels",
                time_launches(iters, [&](int i) {
-                   cx_launch(k_bare_down_item<true>, dim3(112, 9), dim3(256), 0u, (hipStream_t)0, sets[i % 16], sink);
+                   cx_launch(k_bare_down_item<1>, dim3(112, 9), dim3(256), 0u, (hipStream_t)0, sets[i % 16], sink);
+               }), 9.0 * kMat);
+        report("  same bytes as 16-column k-panels",
+               time_launches(iters, [&](int i) {
+                   cx_launch(k_bare_down_item<2>, dim3(112, 9), dim3(256), 0u, (hipStream_t)0, sets[i % 16], sink);
                }), 9.0 * kMat);
         report("bare stream, k_down_comb1 shape (16 rows x all items)",
                time_launches(iters, [&](int i) {
-                   cx_launch(k_bare_down_rows<false>, dim3(kH / 16), dim3(512), 0u, (hipStream_t)0, sets[i % 16], sink);
+                   cx_launch(k_bare_down_rows<0>, dim3(kH / 16), dim3(512), 0u, (hipStream_t)0, sets[i % 16], sink);
                }), 9.0 * kMat);
         report("  same bytes as 32-column k-panels",
                time_launches(iters, [&](int i) {
-                   cx_launch(k_bare_down_rows<true>, dim3(kH / 16), dim3(512), 0u, (hipStream_t)0, sets[i % 16], sink);
+                   cx_launch(k_bare_down_rows<1>, dim3(kH / 16), dim3(512), 0u, (hipStream_t)0, sets[i % 16], sink);
+               }), 9.0 * kMat);
+        report("  same bytes as 16-column k-panels",
+               time_launches(iters, [&](int i) {
+                   cx_launch(k_bare_down_rows<2>, dim3(kH / 16), dim3(512), 0u, (hipStream_t)0, sets[i % 16], sink);
                }), 9.0 * kMat);
         report("k_down_comb1 (down + combine)", time_launches(iters, [&](int i) {
                    ExpertLaunch L = dp.launch(i, table, lds);
