@@ -8,11 +8,15 @@
 // Why this shape.  The activations of an item (x rows for gate/up, h rows for
 // down) are shared by every weight row of the tile, so they go through LDS.
 // For each 128-column k-block, the workgroup's waves each load a share of
-// the item's activation block into registers (gate/up: half a 1 KB "piece"
-// per wave; down: one piece per wave and h plane).  They issue
+// the item's activation block into registers (gate/up: 512 B per wave;
+// down: 1 KB per wave and h plane), whole pairs' 256-byte rows or halves
+// of them, so that every load instruction reads whole 128-byte lines (a
+// share cut along the MFMA fragments instead touched twice to four times
+// as many lines and measured 5-8 % slower).  They issue
 // it together with that k-block's weights, D k-blocks ahead, in the same
-// register ring.  Just before the k-block is used, the pieces are written
-// to one of two LDS slots and a barrier publishes them.  Every vector load
+// register ring.  Just before the k-block is used, each lane writes its
+// piece where the MFMA fragments read it, in one of two LDS slots, and a
+// barrier publishes them.  Every vector load
 // in the loop is an ordinary load of the same kind, so the in-order vmcnt
 // wait that makes a k-block's weights usable also covers its activations.
 // The compiler keeps exact waits across the rolled loop.  Direct
@@ -31,9 +35,9 @@ constexpr size_t kPiece = 1024;                      // one wave load (64 x 16 B
 constexpr size_t kActBlk = 4 * kPiece;               // 16 pairs x 128 k x 16 bit
 
 // gate/up: 8 waves x 16 rows of gate and of up, D-deep register ring; two
-// LDS slots of kGrpTiles activation blocks.  Each wave loads half a piece
-// (8 B per lane) of every column tile per k-block, so one activation block
-// serves 128 weight rows.
+// LDS slots of kGrpTiles activation blocks.  Each wave loads two pairs'
+// rows (8 B per lane) of every column tile per k-block, so one activation
+// block serves 128 weight rows.
 constexpr int kGuGrpWaves = 8;
 constexpr int kGuGrpRows = kTileRows * kGuGrpWaves;  // 128
 constexpr int kGuGrpD = 4;
@@ -165,16 +169,22 @@ __device__ __forceinline__ void grp_gate_up_item(const ExpertLaunch& L, const Un
     const int rbu = __builtin_amdgcn_readfirstlane(r0 / u.e.up_rb);
     float scg_v = lane < NKB ? ldf(u.e.s_gate + (size_t)rbg * NKB + lane) : 0.f;
     float scu_v = lane < NKB ? ldf(u.e.s_up + (size_t)rbu * NKB + lane) : 0.f;
-    // activation pieces: wave w loads half h = w % 2 of piece j = w / 2 of
-    // every column tile; lane (c, g) carries pair tt*16 + c, elements
-    // 8*(4g + j) + 4h .. +3.
-    const int pj = wave >> 1, ph = wave & 1;
+    // activations of a column tile and k-block: 16 pairs x 128 elements.
+    // Wave w loads pairs 2w and 2w + 1 whole (256 B each), so each load
+    // instruction reads 4 whole 128-byte lines; lane l takes pair xp,
+    // elements xe .. +4, and publishes them where the MFMA fragment of
+    // (pair xp, k = 32 g + 8 j) is read from: piece j, lane (g, xp), half.
+    // (These writes land 16 lanes on 2-4 LDS bank groups; an XOR swizzle of
+    // the slots that spread them measured no faster, so the fragment reads
+    // keep their plain lane order.)
+    const int xp = 2 * wave + (lane >> 5), xe = 4 * (lane & 31);
+    const size_t xdst = (size_t)((xe & 31) >> 3) * kPiece + (size_t)((xe >> 5) * 16 + xp) * 16 + 8 * ((xe & 7) >> 2);
     const uint16_t* xs[NT];
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) {
-        const int q = min(tt * kTileTok + c, u.np - 1);
+        const int q = min(tt * kTileTok + xp, u.np - 1);
         const int tok = SINGLE ? u.pb + q : ldi(L.plan.pair_token + u.pb + q);
-        xs[tt] = static_cast<const uint16_t*>(L.x) + (size_t)tok * H + 8 * (4 * g + pj) + 4 * ph;
+        xs[tt] = static_cast<const uint16_t*>(L.x) + (size_t)tok * H + xe;
     }
     u32x4 wb[D][4];
     u32x2 xr[D][NT];
@@ -193,7 +203,7 @@ __device__ __forceinline__ void grp_gate_up_item(const ExpertLaunch& L, const Un
         for (int tt = 0; tt < NT; ++tt) xr[s][tt] = ld8(xs[tt] + (size_t)k * kKB);
     };
     auto publish = [&](int s, int slot) {
-        unsigned char* dst = lds + (size_t)slot * SLOT + pj * kPiece + lane * 16 + 8 * ph;
+        unsigned char* dst = lds + (size_t)slot * SLOT + xdst;
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt) *reinterpret_cast<u32x2*>(dst + tt * kActBlk) = xr[s][tt];
     };
@@ -283,13 +293,17 @@ __device__ __forceinline__ void grp_gate_up_item_c1(const ExpertLaunch& L, const
     const int rbu = __builtin_amdgcn_readfirstlane(r0 / u.e.up_rb);
     float scg_v = lane < NKB ? ldf(u.e.s_gate + (size_t)rbg * NKB + lane) : 0.f;
     float scu_v = lane < NKB ? ldf(u.e.s_up + (size_t)rbu * NKB + lane) : 0.f;
-    // chunk loader: thread (wave w, lane (c, g)) carries piece j = w % 4 of
-    // k-blocks w / 4 + 2i (i < 7) of the chunk for pair c: 16 B each
-    const int q = min(c, u.np - 1);
+    // chunk loader: wave w carries pairs 4 (w % 4) .. +4 whole (256 B each,
+    // one 1 KB load instruction = 8 whole 128-byte lines) of k-blocks
+    // w / 4 + 2i (i < 7) of the chunk; lane l takes pair xp, elements
+    // xe .. +8, published where the MFMA fragment of (pair xp,
+    // k = 32 g + 8 j) is read from: piece j, lane (g, xp)
+    const int xp = 4 * (wave & 3) + (lane >> 4), xe = 8 * (lane & 15);
+    const int q = min(xp, u.np - 1);
     const int tok = SINGLE ? u.pb + q : ldi(L.plan.pair_token + u.pb + q);
-    const int pj = wave & 3, kq = wave >> 2;
-    const uint16_t* xs = static_cast<const uint16_t*>(L.x) + (size_t)tok * H + 8 * (4 * g + pj);
-    unsigned char* xdst = lds + pj * kPiece + lane * 16;
+    const int kq = wave >> 2;
+    const uint16_t* xs = static_cast<const uint16_t*>(L.x) + (size_t)tok * H + xe;
+    unsigned char* xdst = lds + (size_t)((xe & 31) >> 3) * kPiece + (size_t)((xe >> 5) * 16 + xp) * 16;
     u32x4 xr[XL];
     // chunk loads from a base advanced per chunk (kept opaque so the offsets
     // stay immediates instead of one precomputed address per load)
@@ -443,14 +457,23 @@ __device__ __forceinline__ void grp_down_item(const ExpertLaunch& L, const Unit&
     const int rb1 = __builtin_amdgcn_readfirstlane((rw + kTileRows) / u.e.down_rb);
     float sd0_v = lane < NKB ? ldf(u.e.s_down + (size_t)rb0 * NKB + lane) : 0.f;
     float sd1_v = lane < NKB ? ldf(u.e.s_down + (size_t)rb1 * NKB + lane) : 0.f;
-    // h pieces: wave w loads plane w / 4 (hi, lo), piece j = w % 4 of every
-    // column tile.
+    // h of a column tile and k-block: 16 pairs x 128 elements per plane.
+    // Wave w loads plane w / 4 (hi, lo), quarter j = w % 4: pairs
+    // 8 (j >> 1) .. +8, elements 64 (j & 1) .. +64 of each, so each load
+    // instruction reads 8 whole 128-byte lines; lane l takes pair hp,
+    // elements hk0 .. +8, and publishes them where the MFMA fragment of
+    // (pair hp, k = 32 g + 8 j) is read from: piece (hk0 % 32) / 8, lane
+    // (hk0 / 32, hp).
     const int plane = wave >> 2, pj = wave & 3;
+    const int hp = 8 * (pj >> 1) + (lane >> 3);
+    const int hk0 = 64 * (pj & 1) + 8 * (lane & 7);
+    const size_t hdst = (size_t)plane * PLANE + (size_t)((hk0 & 31) >> 3) * kPiece +
+                        (size_t)((hk0 >> 5) * 16 + hp) * 16;
     const uint16_t* hs[NT];
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) {
-        const int q = min(tt * kTileTok + c, u.np - 1);
-        hs[tt] = (plane ? L.h_lo : L.h_hi) + (size_t)(u.pb + q) * I + 8 * (4 * g + pj);
+        const int q = min(tt * kTileTok + hp, u.np - 1);
+        hs[tt] = (plane ? L.h_lo : L.h_hi) + (size_t)(u.pb + q) * I + hk0;
     }
     u32x4 wb[D][4];
     u32x4 hr[D][NT];
@@ -469,7 +492,7 @@ __device__ __forceinline__ void grp_down_item(const ExpertLaunch& L, const Unit&
         for (int tt = 0; tt < NT; ++tt) hr[s][tt] = ld16(hs[tt] + (size_t)k * kKB);
     };
     auto publish = [&](int s, int slot) {
-        unsigned char* dst = lds + (size_t)slot * SLOT + plane * PLANE + pj * kPiece + lane * 16;
+        unsigned char* dst = lds + (size_t)slot * SLOT + hdst;
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt) *reinterpret_cast<u32x4*>(dst + tt * kActBlk) = hr[s][tt];
     };
@@ -517,8 +540,9 @@ __device__ __forceinline__ void grp_down_item(const ExpertLaunch& L, const Unit&
             if (q < u.np) {
                 const size_t p = (size_t)(u.pb + q);
                 const f32x4 v = acc[a][tt];
+                // y_part is read once, by the combine launch: streamed stores
                 if (SINGLE) store_out4(L.y, L.y_f32, p * H + row, v, L.out_dtype);
-                else *reinterpret_cast<float4*>(L.y_part + p * H + row) = float4{v[0], v[1], v[2], v[3]};
+                else __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(L.y_part + p * H + row));
             }
         }
     }

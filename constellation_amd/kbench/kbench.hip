@@ -16,6 +16,8 @@
 //                          handed out statically or claimed from per-XCD counters,
 //                          and k_down_comb1 over 256 / 384 / 448 / 512 tiles
 //   cx_kbench grouped      the grouped prefill kernels on the config-3-like plan
+//   cx_kbench grouped-down the plan's down bytes streamed bare in the grouped down
+//                          kernel's shape, by tiles per workgroup and occupancy
 //   cx_kbench fused1       one expert, one token: one launch split over inter (w_down
 //                          as k-panels) + a reduce launch, against the two launches
 //   cx_kbench rates        per-CU rates the LDS-ring kernels are built on, in shader
@@ -704,6 +706,96 @@ int cmd_layout(int iters) {
     return 0;
 }
 
+// Bare streams of a prefill plan's down bytes in the grouped down kernel's
+// shape: 256-row workgroups (8 waves x 32 rows as two 16-row tiles), full-K
+// waves (16 k-blocks), a 4-deep register ring, no compute.  Each workgroup
+// takes M consecutive 256-row tiles of one item, the ring running on from
+// one tile into the next (so a workgroup ramps up and drains once per M
+// tiles).  Launched with 100 KB of dynamic LDS it runs one workgroup per CU,
+// as the grouped down kernel does (242 VGPRs).
+// ST: after its stream, each workgroup writes its 256 rows of every pair of
+// the item into y_part (fp32, streamed stores), as the grouped down does.
+template <int M, bool ST = false>
+__global__ __launch_bounds__(512) void k_bare_dn(ExpertLaunch L, uint32_t* sink) {
+    constexpr int NKB = 16, D = 4, WPI = kH / 256 / M;  // workgroups per item
+    static_assert(kH % (256 * M) == 0, "tiles per workgroup divide the item's tiles");
+    extern __shared__ uint32_t dyn_lds[];
+    const int wg = blockIdx.x % WPI, item = blockIdx.x / WPI;
+    const int wave = wave_id(), lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+    const ItemRec r = ld_uniform(L.plan.item_rec + item);
+    auto at = [&](int k, int half) {
+        const int t = wg * M + k / NKB;
+        return r.w_down + (size_t)(t * 256 + wave * 32 + half * 16 + c) * kI + (size_t)(k % NKB) * kKB + g * 32;
+    };
+    u32x4 wb[D][4];
+    uint32_t acc = 0;
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+        wb[s][0] = ld16(at(s, 0));
+        wb[s][1] = ld16(at(s, 0) + 16);
+        wb[s][2] = ld16(at(s, 1));
+        wb[s][3] = ld16(at(s, 1) + 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll 4
+    for (int k = 0; k < M * NKB; ++k) {
+        const int s = k % D;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc ^= wb[s][j][0] + wb[s][j][1] * 3u + wb[s][j][2] * 5u + wb[s][j][3] * 7u;
+        if (k + D < M * NKB) {
+            __builtin_amdgcn_sched_barrier(0);
+            wb[s][0] = ld16(at(k + D, 0));
+            wb[s][1] = ld16(at(k + D, 0) + 16);
+            wb[s][2] = ld16(at(k + D, 1));
+            wb[s][3] = ld16(at(k + D, 1) + 16);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    if (ST) {
+        const f32x4 v = {(float)(acc & 0xff), 0.f, 0.f, 0.f};
+        for (int t = 0; t < M; ++t)
+            for (int q = c; q < r.np; q += 16)
+                for (int a = 0; a < 2; ++a)
+                    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(
+                        L.y_part + (size_t)(r.pb + q) * kH + (wg * M + t) * 256 + wave * 32 + a * 16 + 4 * g));
+    } else if (acc == 0x12345678u) {
+        dyn_lds[threadIdx.x] = acc;
+        sink[threadIdx.x] = dyn_lds[(threadIdx.x + 1) & 511];
+    }
+}
+
+int cmd_grouped_down(int iters) {
+    Pool pool(true);
+    std::vector<PrefillPlan> plans;
+    for (int l = 0; l < 4; ++l) plans.emplace_back(pool, 5 + l);
+    std::printf("grouped-down: config-3-like plan, %d items, experts spread over 24 x 2 GiB\n", plans[0].n_items);
+    uint32_t* sink = nullptr;
+    KB_CHECK(hipMalloc(&sink, 4096));
+    const double streamed = (double)plans[0].n_items * kMat;  // every item streams its expert's down matrix
+    const double dn = 257.0 * kMat + 4608.0 * kH * 4;
+    const uint32_t one_per_cu = 100u * 1024u;
+    auto bare = [&](const char* what, auto kernel, int m, uint32_t lds) {
+        report(what, time_launches(iters, [&](int i) {
+                   const PrefillPlan& p = plans[i % 4];
+                   cx_launch(kernel, dim3(kH / 256 / m * p.n_items), dim3(512), lds, (hipStream_t)0, p.L, sink);
+               }), streamed);
+    };
+    for (int rep = 0; rep < 2; ++rep) {
+        std::printf(" pass %d (bare lines: bytes streamed = items x down matrix)\n", rep + 1);
+        bare("bare down, 1 tile per workgroup, occupancy free", k_bare_dn<1>, 1, 0u);
+        bare("bare down, 1 tile per workgroup, 1 workgroup per CU", k_bare_dn<1>, 1, one_per_cu);
+        bare("bare down, 2 tiles per workgroup, 1 workgroup per CU", k_bare_dn<2>, 2, one_per_cu);
+        bare("bare down, 4 tiles per workgroup, 1 workgroup per CU", k_bare_dn<4>, 4, one_per_cu);
+        bare("bare down, 7 tiles per workgroup, 1 workgroup per CU", k_bare_dn<7>, 7, one_per_cu);
+        bare("bare down + the fp32 y_part stores, 1 tile per workgroup", k_bare_dn<1, true>, 1, one_per_cu);
+        report("k_dn_grp (algorithmic bytes)", time_launches(iters, [&](int i) {
+                   KB_CHECK(launch_down(plans[i % 4].L, 0));
+               }), dn);
+    }
+    (void)hipFree(sink);
+    return 0;
+}
+
 int cmd_grouped(int iters) {
     Pool pool(true);
     std::vector<PrefillPlan> plans;
@@ -1046,6 +1138,7 @@ int main(int argc, char** argv) {
     if (!std::strcmp(cmd, "placement")) return cmd_placement(iters);
     if (!std::strcmp(cmd, "decode-balance")) return cmd_decode_balance(iters);
     if (!std::strcmp(cmd, "grouped")) return cmd_grouped(std::min(iters, 12));
+    if (!std::strcmp(cmd, "grouped-down")) return cmd_grouped_down(std::min(iters, 12));
     if (!std::strcmp(cmd, "rates")) return cmd_rates(iters);
     if (!std::strcmp(cmd, "fused1")) return cmd_fused1(iters);
     std::fprintf(stderr, "usage: cx_kbench layout|decode-down|placement|decode-balance|grouped|rates|fused1 [launches]\n");
