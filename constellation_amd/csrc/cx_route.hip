@@ -675,20 +675,35 @@ __device__ __forceinline__ bool dup_route(const int32_t* ids, int i, int top_k) 
 // <= item_cap pairs, routed items first.  The order of pairs inside a slot
 // only picks an MFMA column, which never changes a value, so the atomic
 // cursor keeps the results deterministic.  LDS: 2*E + blockDim ints.
-__device__ __forceinline__ int block_excl_scan(int v, int* tmp, int* total) {
-    const int tid = threadIdx.x, n = blockDim.x;
-    tmp[tid] = v;
-    __syncthreads();
-    for (int off = 1; off < n; off <<= 1) {
-        const int a = tid >= off ? tmp[tid - off] : 0;
-        __syncthreads();
-        tmp[tid] += a;
-        __syncthreads();
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int a = __shfl_up(v, off, 64);
+        if (lane >= off) v += a;
     }
-    const int incl = tmp[tid];
-    *total = tmp[n - 1];
+    return v;
+}
+
+// Exclusive scan over the workgroup (blockDim a multiple of 64, at most
+// 4096): a scan inside each wave, the waves' totals scanned by wave 0, three
+// barriers in all.  tmp: >= 129 ints.
+__device__ __forceinline__ int block_excl_scan(int v, int* tmp, int* total) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
+    const int incl = wave_incl_scan(v);
+    if (lane == 63) tmp[wv] = incl;
     __syncthreads();
-    return incl - v;
+    if (wv == 0) {
+        const int t = lane < nw ? tmp[lane] : 0;
+        const int ti = wave_incl_scan(t);
+        if (lane < nw) tmp[64 + lane] = ti - t;
+        if (lane == 63) tmp[128] = ti;
+    }
+    __syncthreads();
+    const int res = incl - v + tmp[64 + wv];
+    *total = tmp[128];
+    __syncthreads();
+    return res;
 }
 
 __device__ __forceinline__ void plan_build(const int32_t* __restrict__ ids, const float* __restrict__ w,
