@@ -627,35 +627,52 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void k
 // ---------------------------------------------------------------------------
 // Combine: y[t] = sum_k w_k * y_part[pair(t,k)]  (route order, fp32)
 //               + y_part[pair(t, shared)]
-// then cast (RNE).  One thread per 4 consecutive features.
+// then cast (RNE).  One thread per 4 consecutive features.  A token's pair
+// indices come in one round trip and every weight and partial row it needs
+// (KC routes at a time, the shared expert's row with the first batch) in a
+// second; a route the planner dropped (pair -1) contributes nothing.
 __global__ __launch_bounds__(256) void k_combine(PlanPtrs plan, const float* __restrict__ y_part,
                                                  int n_tokens, int top_k, int hidden, void* y,
                                                  int out_dtype, float* y_f32) {
+    constexpr int KC = 8;  // routes fetched per batch
     const int n4 = hidden / 4;
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= n_tokens * n4) return;
     const int t = idx / n4;
     const int f = (idx - t * n4) * 4;
     const int* tp = plan.token_pairs + (size_t)t * (top_k + 1);
+    const int ps = tp[top_k];
+    float4 vs = {0.f, 0.f, 0.f, 0.f};
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int k = 0; k < top_k; ++k) {
-        const int p = tp[k];
-        if (p >= 0) {
-            const float w = plan.pair_weight[p];
-            const float4 v = *reinterpret_cast<const float4*>(y_part + (size_t)p * hidden + f);
-            acc[0] += w * v.x;
-            acc[1] += w * v.y;
-            acc[2] += w * v.z;
-            acc[3] += w * v.w;
+    for (int k0 = 0; k0 < top_k; k0 += KC) {
+        int p[KC];
+#pragma unroll
+        for (int j = 0; j < KC; ++j) p[j] = k0 + j < top_k ? tp[k0 + j] : -1;
+        float w[KC];
+        float4 v[KC];
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            const size_t q = p[j] >= 0 ? (size_t)p[j] : 0;
+            w[j] = plan.pair_weight[q];
+            v[j] = *reinterpret_cast<const float4*>(y_part + q * hidden + f);
+        }
+        if (k0 == 0 && ps >= 0) vs = *reinterpret_cast<const float4*>(y_part + (size_t)ps * hidden + f);
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            if (p[j] >= 0) {
+                acc[0] += w[j] * v[j].x;
+                acc[1] += w[j] * v[j].y;
+                acc[2] += w[j] * v[j].z;
+                acc[3] += w[j] * v[j].w;
+            }
         }
     }
-    const int ps = tp[top_k];
     if (ps >= 0) {
-        const float4 v = *reinterpret_cast<const float4*>(y_part + (size_t)ps * hidden + f);
-        acc[0] += v.x;
-        acc[1] += v.y;
-        acc[2] += v.z;
-        acc[3] += v.w;
+        if (top_k <= 0) vs = *reinterpret_cast<const float4*>(y_part + (size_t)ps * hidden + f);
+        acc[0] += vs.x;
+        acc[1] += vs.y;
+        acc[2] += vs.z;
+        acc[3] += vs.w;
     }
     uint16_t* yo = static_cast<uint16_t*>(y) + (size_t)t * hidden + f;
     const uint2 o = {cast_out(acc[0], out_dtype) | (cast_out(acc[1], out_dtype) << 16),
