@@ -52,11 +52,12 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU baseline time budget")
     ap.add_argument("--no-extra-configs", action="store_true",
                     help="skip the single-expert, prefill and node-share measurements")
-    ap.add_argument("--extras", default="h,0,3,c,4",
+    ap.add_argument("--extras", default="h,p,0,3,c,4",
                     help="comma list of the extra measurements: h host boundary at B=1 "
-                         "(layer request vs per-expert requests), 0 single expert, "
-                         "3 prefill chunk, c compute-bound prefill shape (not a BASELINE "
-                         "config), 4 node share (default: all)")
+                         "(layer request vs per-expert requests), p the B=1 layer through "
+                         "the fused and the staged pipeline (interleaved A/B), 0 single "
+                         "expert, 3 prefill chunk, c compute-bound prefill shape (not a "
+                         "BASELINE config), 4 node share (default: all)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="first run a plain device copy of this many MiB (three times): the "
                          "known-size kernel that scales HBM counters of a --pmc profile")
@@ -107,13 +108,54 @@ def build_layers(ctx, n_layers):
     return layers
 
 
-def run_steps(ctx, layers, pool, T, steps, outs):
+def run_steps(ctx, layers, pool, T, steps, outs, resident=None):
     for i in range(steps):
         L = layers[i % len(layers)]
         p0 = (i * T) % (pool.shape[0] - T + 1)
-        ctx.moe_layer(L["layer"], pool[p0:p0 + T], L["w_r"], L["bias"], n_group=NGROUP,
-                      topk_group=TOPK_GROUP, top_k=TOPK, norm_topk_prob=True,
+        ctx.moe_layer(L["layer"], pool[p0:p0 + T], L["w_r"], L["bias"], resident=resident,
+                      n_group=NGROUP, topk_group=TOPK_GROUP, top_k=TOPK, norm_topk_prob=True,
                       routed_scaling_factor=SCALE, out=outs)
+
+
+def bench_b1_pipelines(ctx, layers, pool, steps, reps=3):
+    """The B=1 layer through its two pipelines in one process, interleaved:
+    'fused' (the default: logits + shared gate/up, routed gate/up with the
+    selection inside, down + combine) and 'staged' (forced by a resident
+    mask of all ones, which selects the same experts: logits, selection +
+    shared gate/up, routed gate/up, down + combine).  Per pipeline: the
+    median over `reps` of the wall time per step and of each launch's
+    HIP-event span."""
+    import statistics
+    import torch
+    dev = pool.device
+    ones = torch.ones(E, dtype=torch.uint8, device=dev)
+    outs = (torch.empty((1, H), dtype=torch.bfloat16, device=dev), None,
+            torch.empty((1, TOPK), dtype=torch.int32, device=dev),
+            torch.empty((1, TOPK), dtype=torch.float32, device=dev))
+    res = {"fused": {"wall": [], "kernels": {}}, "staged": {"wall": [], "kernels": {}}}
+    for mask in (None, ones):
+        run_steps(ctx, layers, pool, 1, 40, outs, mask)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        for name, mask in (("fused", None), ("staged", ones)):
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record()
+            run_steps(ctx, layers, pool, 1, steps, outs, mask)
+            ev1.record()
+            torch.cuda.synchronize()
+            res[name]["wall"].append(ev0.elapsed_time(ev1) / steps * 1e3)
+            ctx.profile(True)
+            run_steps(ctx, layers, pool, 1, steps // 2, outs, mask)
+            torch.cuda.synchronize()
+            for k in ("route", "plan", "gate_up", "down"):
+                n, ms = ctx.profile_read(k)
+                if n:
+                    res[name]["kernels"].setdefault(k, []).append(ms * 1e3 / n)
+            ctx.profile(False)
+    ctx.sync()
+    return {name: {"us_per_token": statistics.median(r["wall"]),
+                   "kernels_us": {k: statistics.median(v) for k, v in r["kernels"].items()}}
+            for name, r in res.items()}
 
 
 def time_config(ctx, layers, pool, T, steps, warmup):
@@ -568,6 +610,8 @@ def main() -> int:
     want = set() if args.no_extra_configs else {c.strip() for c in args.extras.split(",") if c.strip()}
     if "h" in want:
         extras["b1"]["host_boundary"] = bench_host_boundary(ctx, layers, pool, 100)
+    if "p" in want:
+        extras["b1"]["pipelines"] = bench_b1_pipelines(ctx, layers, pool, 400)
     if "0" in want:
         extras["config0_single_expert"] = bench_single_expert(ctx, layers, max(100, args.steps // 2))
     if "3" in want:
