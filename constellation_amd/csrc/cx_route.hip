@@ -1530,29 +1530,69 @@ __device__ __forceinline__ void groups256(double c[4], int topk_group) {
     for (int i = 0; i < 4; ++i) c[i] = keep ? c[i] : -INFINITY;
 }
 
-// Pick stage: the top_k largest remaining scores, in order.
-__device__ __forceinline__ Picks8 picks256(double c[4], int top_k) {
+// Pick stage: the top_k largest remaining scores, in order.  The rounds run
+// on 32-bit unsigned keys with the order of float(c) (rounding is monotonic,
+// so the largest c holds the largest key): one DPP max per reduction step
+// (bound_ctrl: a lane with no source reads 0, below every key) and the
+// per-slot matches as ballots of the compares.  A round whose largest key is
+// held by one entry alone is decided by it; otherwise (equal c, or c values
+// closer than float resolution) the exact fp64 arg-max over the entries
+// holding that key decides, ties to the lower expert index.  The same picks
+// as a fp64 reduction per round, in about two thirds of its time.
+template <int CTRL, int RM, int BM>
+__device__ __forceinline__ uint32_t dpp_umax(uint32_t v) {
+    const uint32_t o = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, RM, BM, true));
+    return v > o ? v : o;
+}
+
+__device__ __forceinline__ uint32_t order_key(double c) {
+    const uint32_t b = __float_as_uint(static_cast<float>(c));
+    return b ^ ((b >> 31) ? 0xFFFFFFFFu : 0x80000000u);
+}
+
+__device__ __forceinline__ Picks8 picks256(const double c[4], int top_k) {
     const int lane = threadIdx.x & 63;
+    uint32_t k[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) k[i] = order_key(c[i]);
     Picks8 p;
 #pragma unroll
     for (int r = 0; r < kSel256MaxPicks; ++r) {
         p.id[r] = -1;
         if (r < top_k) {
-            double m = max_d(max_d(c[0], c[1]), max_d(c[2], c[3]));
-            m = max_d(m, dpp_d<0x111, 0xF, 0xF>(m));
-            m = max_d(m, dpp_d<0x112, 0xF, 0xF>(m));
-            m = max_d(m, dpp_d<0x114, 0xF, 0xF>(m));
-            m = max_d(m, dpp_d<0x118, 0xF, 0xF>(m));
-            m = max_d(m, dpp_d<0x142, 0xA, 0xF>(m));
-            m = max_d(m, dpp_d<0x143, 0xC, 0xF>(m));
-            const double M = readlane_d(m, 63);
-            const int fs = c[0] == M ? 0 : c[1] == M ? 1 : c[2] == M ? 2 : c[3] == M ? 3 : 4;
-            const unsigned long long hit = __ballot(fs < 4);
-            const int owner = static_cast<int>(__builtin_ctzll(hit));
-            const int slot = __builtin_amdgcn_readlane(fs, owner);
-            p.id[r] = owner * 4 + slot;
+            uint32_t m = max(max(k[0], k[1]), max(k[2], k[3]));
+            m = dpp_umax<0x111, 0xF, 0xF>(m);
+            m = dpp_umax<0x112, 0xF, 0xF>(m);
+            m = dpp_umax<0x114, 0xF, 0xF>(m);
+            m = dpp_umax<0x118, 0xF, 0xF>(m);
+            m = dpp_umax<0x142, 0xA, 0xF>(m);
+            m = dpp_umax<0x143, 0xC, 0xF>(m);
+            const uint32_t M = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), 63));
+            unsigned long long h[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) c[i] = (lane == owner && i == slot) ? -INFINITY : c[i];
+            for (int i = 0; i < 4; ++i) h[i] = __ballot(k[i] == M);
+            const int n = __popcll(h[0]) + __popcll(h[1]) + __popcll(h[2]) + __popcll(h[3]);
+            int pick = 0x7fffffff;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (h[i]) pick = min(pick, 4 * static_cast<int>(__builtin_ctzll(h[i])) + i);
+            if (n != 1) {
+                double v = -INFINITY;
+                int vi = 0x7fffffff;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (k[q] == M && better(c[q], 4 * lane + q, v, vi)) {
+                        v = c[q];
+                        vi = 4 * lane + q;
+                    }
+                wave_argmax(v, vi);
+                pick = vi;
+            }
+            // NaN scores (from NaN inputs) match no key: pick a valid id
+            pick = pick >= 0 && pick < kSel256Experts ? pick : 0;
+            p.id[r] = pick;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) k[i] = 4 * lane + i == pick ? 0u : k[i];
         }
     }
     return p;

@@ -565,6 +565,44 @@ def test_one_token_fused_selection_equals_staged(gpu, oracle, E, H, I, shared, T
         _free(layer, experts, sh)
 
 
+def test_one_token_fused_selection_ties(gpu, oracle):
+    """The fused one-token selection decides most picks on float keys and
+    falls back to exact fp64 when the largest key is shared.  Router rows
+    that saturate the sigmoid (s = 1 exactly) and chosen biases make the
+    choice scores c = 1 + bias: an exact 3-way tie (experts 100-102), a
+    pair 2^-41 apart (41 above 40: one float key, two fp64 values), an
+    exact 2-way tie (3, 7) and a distinct pair (200 above 201), in four
+    groups.  The picks must come in c order, ties to the lower index, and
+    equal the staged pipeline's; all eight weights equal."""
+    print("[moe] fused selection ties", flush=True)
+    E, H, I = 256, 1024, 512
+    layer, experts, sh, _, _ = _make_layer(gpu, oracle, E, H, I, seed=98, shared=True)
+    try:
+        x, w, bias = _router_inputs(gpu, 99, 1, E, H)
+        boost = torch.where(x[0] >= 0, 0.05, -0.05).to(torch.bfloat16)
+        u = 2.0 ** -20
+        plan = {100: 5 * u, 101: 5 * u, 102: 5 * u, 40: 4 * u, 41: 4 * u + 2.0 ** -41,
+                3: 3 * u, 7: 3 * u, 200: 2 * u, 201: u}
+        for e, b in plan.items():
+            w[e] = boost
+            bias[e] = b
+        assert float(bias[41]) != float(bias[40])  # representable apart in fp32
+        ones = torch.ones(E, dtype=torch.uint8, device="cuda")
+        a = gpu.moe_layer(layer, x, w, bias, n_group=8, topk_group=4, top_k=8, want_f32=True)
+        b = gpu.moe_layer(layer, x, w, bias, resident=ones, n_group=8, topk_group=4, top_k=8,
+                          want_f32=True)
+        gpu.sync()
+        ya, yfa, ida, wa = (t.cpu() for t in a)
+        yb, yfb, idb, wb = (t.cpu() for t in b)
+        assert ida[0].tolist() == [100, 101, 102, 41, 40, 3, 7, 200], ida
+        assert torch.equal(ida, idb)
+        assert torch.equal(wa, wb) and torch.all(wa == wa[0, 0])
+        assert torch.equal(yfa.view(torch.int32), yfb.view(torch.int32))
+        assert torch.equal(ya.view(torch.int16), yb.view(torch.int16))
+    finally:
+        _free(layer, experts, sh)
+
+
 @pytest.mark.parametrize("T,dtype", [(1, torch.float16), (7, torch.bfloat16), (16, torch.float16)])
 def test_moe_decode_given_routes_with_shared(gpu, oracle, T, dtype):
     """cx_moe_decode (routes given): planner beside the shared expert's gate/up,
