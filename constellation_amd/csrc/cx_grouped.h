@@ -177,6 +177,7 @@ __device__ __forceinline__ void grp_gate_up_item(const ExpertLaunch& L, const Un
     // (These writes land 16 lanes on 2-4 LDS bank groups; an XOR swizzle of
     // the slots that spread them measured no faster, so the fragment reads
     // keep their plain lane order.)
+    static_assert(kGuGrpWaves * 2 == kTileTok, "two pairs per wave cover a column tile");
     const int xp = 2 * wave + (lane >> 5), xe = 4 * (lane & 31);
     const size_t xdst = (size_t)((xe & 31) >> 3) * kPiece + (size_t)((xe >> 5) * 16 + xp) * 16 + 8 * ((xe & 7) >> 2);
     const uint16_t* xs[NT];
@@ -464,6 +465,7 @@ __device__ __forceinline__ void grp_down_item(const ExpertLaunch& L, const Unit&
     // elements hk0 .. +8, and publishes them where the MFMA fragment of
     // (pair hp, k = 32 g + 8 j) is read from: piece (hk0 % 32) / 8, lane
     // (hk0 / 32, hp).
+    static_assert(kDnGrpWaves == 8, "h loader: 2 planes x 4 quarters of 8 pairs x 64 elements");
     const int plane = wave >> 2, pj = wave & 3;
     const int hp = 8 * (pj >> 1) + (lane >> 3);
     const int hk0 = 64 * (pj & 1) + 8 * (lane & 7);
