@@ -40,6 +40,7 @@ class ExpertDesc(C.Structure):
         ("up_rb", C.c_int32), ("up_cb", C.c_int32),
         ("gate_rb", C.c_int32), ("gate_cb", C.c_int32),
         ("down_rb", C.c_int32), ("down_cb", C.c_int32),
+        ("gu_layout", C.c_int32), ("reserved", C.c_int32 * 3),
     ]
 
 
@@ -71,6 +72,8 @@ _SIGS = {
     "cx_device_query": (_I, [_I, C.POINTER(DeviceInfo)]),
     "cx_upload_matrix": (_I, [_I, _P, C.c_uint64, C.c_uint64, _P, C.c_uint64,
                               C.POINTER(_P), C.POINTER(_P)]),
+    "cx_upload_matrix_tiled": (_I, [_I, _P, C.c_uint64, C.c_uint64, _P, C.c_uint64,
+                                    C.POINTER(_P), C.POINTER(_P)]),
     "cx_free_device": (_I, [_I, _P]),
     "cx_arena_stats": (_I, [_I, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
     "cx_ctx_create": (_I, [_I, C.POINTER(_P)]),

@@ -9,18 +9,20 @@ namespace expert_node_v2 {
 
 namespace {
 
-bool UploadOneMatrixAmd(int device, const MatrixBlockScaleViewV2& view, MatrixMetaV2* meta,
-                        BlockScaleMetaV2* scale_meta, DeviceBufferV2<std::uint8_t>* weight,
-                        DeviceBufferV2<float>* scale) {
+bool UploadOneMatrixAmd(int device, const MatrixBlockScaleViewV2& view, bool gate_up,
+                        MatrixMetaV2* meta, BlockScaleMetaV2* scale_meta,
+                        DeviceBufferV2<std::uint8_t>* weight, DeviceBufferV2<float>* scale) {
     std::uint8_t* dw = nullptr;
     float* ds = nullptr;
-    const int rc = cx_upload_matrix(device, view.weight.data.data(),
-                                    static_cast<std::uint64_t>(view.matrix.rows),
-                                    static_cast<std::uint64_t>(view.matrix.cols),
-                                    view.scale.data.data(), view.scale.data.size(), &dw, &ds);
+    const std::uint64_t rows = static_cast<std::uint64_t>(view.matrix.rows);
+    const std::uint64_t cols = static_cast<std::uint64_t>(view.matrix.cols);
+    const bool tiled = gate_up && AmdGateUpLayout(rows, cols) == CX_LAYOUT_TILE16;
+    const int rc = (tiled ? cx_upload_matrix_tiled : cx_upload_matrix)(
+        device, view.weight.data.data(), rows, cols, view.scale.data.data(), view.scale.data.size(),
+        &dw, &ds);
     if (rc != CX_OK) {
-        std::fprintf(stderr, "[UploadExpertAmdV2] cx_upload_matrix rc=%d: %s\n", rc,
-                     cx_last_error());
+        std::fprintf(stderr, "[UploadExpertAmdV2] %s rc=%d: %s\n",
+                     tiled ? "cx_upload_matrix_tiled" : "cx_upload_matrix", rc, cx_last_error());
         return false;
     }
     *meta = view.matrix;
@@ -53,11 +55,11 @@ bool UploadExpertAmdV2(int local_gpu_id, const ExpertTensorBundleV2& host_bundle
         return false;
     }
     ExpertDeviceStorageV2& s = *out_storage;
-    if (!UploadOneMatrixAmd(local_gpu_id, v.w_up, &s.w_up_meta, &s.w_up_scale_meta,
+    if (!UploadOneMatrixAmd(local_gpu_id, v.w_up, true, &s.w_up_meta, &s.w_up_scale_meta,
                             &s.w_up_weight, &s.w_up_scale) ||
-        !UploadOneMatrixAmd(local_gpu_id, v.w_gate, &s.w_gate_meta, &s.w_gate_scale_meta,
+        !UploadOneMatrixAmd(local_gpu_id, v.w_gate, true, &s.w_gate_meta, &s.w_gate_scale_meta,
                             &s.w_gate_weight, &s.w_gate_scale) ||
-        !UploadOneMatrixAmd(local_gpu_id, v.w_down, &s.w_down_meta, &s.w_down_scale_meta,
+        !UploadOneMatrixAmd(local_gpu_id, v.w_down, false, &s.w_down_meta, &s.w_down_scale_meta,
                             &s.w_down_weight, &s.w_down_scale)) {
         FreeExpertWeightsAmdV2(out_storage);
         return false;

@@ -5,14 +5,26 @@
 // through the C ABI of include/cx_moe.h (libcx_moe.so).
 #pragma once
 
+#include <cstdint>
+
+#include "cx_moe.h"
 #include "expert_node_v2/expert_format_v2.h"
 
 namespace expert_node_v2 {
 
+// How UploadExpertAmdV2 stores w_up and w_gate ([inter, hidden]): re-tiled
+// on the device (CX_LAYOUT_TILE16, cx_upload_matrix_tiled) whenever the shape
+// allows, else row-major.  BackendWorkspaceAmdV2 describes resident experts
+// with the same rule, so the two always agree.
+inline int AmdGateUpLayout(std::uint64_t rows, std::uint64_t cols) {
+    return rows % 16 == 0 && cols % 128 == 0 ? CX_LAYOUT_TILE16 : CX_LAYOUT_ROWS;
+}
+
 // UploadExpertFnV2 (backend_registry_v2.h:21-24).  Validates the bundle with
 // BuildExpertWeightsViewV2, then places each fp8 matrix and its fp32 scales
-// in the device's HBM arena (cx_upload_matrix).  On failure the storage is
-// left fully reset, as the contract requires.
+// in the device's HBM arena (cx_upload_matrix; up and gate through
+// cx_upload_matrix_tiled where AmdGateUpLayout says so).  On failure the
+// storage is left fully reset, as the contract requires.
 bool UploadExpertAmdV2(
     int local_gpu_id,
     const ExpertTensorBundleV2& host_bundle,

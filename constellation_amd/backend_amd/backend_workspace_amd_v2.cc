@@ -7,6 +7,7 @@
 #include <utility>
 
 #include "cx_moe.h"
+#include "expert_node_v2/backend/amd/backend_amd_v2.h"
 
 namespace expert_node_v2 {
 
@@ -46,6 +47,7 @@ cx_expert_desc describe(const ExpertDeviceStorageV2& storage) {
     d.gate_cb = storage.w_gate_scale_meta.col_block;
     d.down_rb = storage.w_down_scale_meta.row_block;
     d.down_cb = storage.w_down_scale_meta.col_block;
+    d.gu_layout = AmdGateUpLayout(storage.w_up_meta.rows, storage.w_up_meta.cols);  // as uploaded
     return d;
 }
 

@@ -172,13 +172,19 @@ __device__ __forceinline__ void big_gate_up(const ExpertLaunch& L, unsigned char
     const int r0 = tile * kBigGuRows;
     // DMA sources.  Weights: instruction i = 2 wave + m fills LDS rows
     // 16 i .. 16 i + 15 (gate rows 0..127, then up), lane -> row 16 i + lane / 4.
+    const int gl = __builtin_amdgcn_readfirstlane(u.e.gu_layout);
     const uint8_t* asrc[2];
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
         const int r = 16 * (2 * wave + m) + (lane >> 2);
         const int q = (lane & 3) ^ ((r >> 1) & 3);
-        asrc[m] = (r < kBigGuRows ? u.e.w_gate : u.e.w_up) + (size_t)(r0 + (r & (kBigGuRows - 1))) * H + 16 * q;
+        asrc[m] = (r < kBigGuRows ? u.e.w_gate : u.e.w_up) + gu_elem_off(gl, H, r0 + (r & (kBigGuRows - 1)), 16 * q);
     }
+    // stage s (64 columns): s * 64 bytes row-major; in 16-row tiles, the
+    // lower or upper half (quarters 0-1 or 2-3) of k-block s / 2
+    auto a_stage = [&](int s) -> size_t {
+        return gl == CX_LAYOUT_TILE16 ? (size_t)(s >> 1) * 2048 + (size_t)(s & 1) * 1024 : (size_t)s * kBigK;
+    };
     // x: instruction i = 2 wave + m fills pairs 8 i .. 8 i + 7, lane -> pair
     // 8 i + lane / 8 (pairs past the item repeat its last row; not stored).
     const uint16_t* bsrc[2];
@@ -203,7 +209,7 @@ __device__ __forceinline__ void big_gate_up(const ExpertLaunch& L, unsigned char
         unsigned char* sb = st[slot];
 #pragma unroll
         for (int m = 0; m < 2; ++m)
-            __builtin_amdgcn_global_load_lds(asrc[m] + (size_t)s * kBigK, sb + (2 * wave + m) * 1024, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(asrc[m] + a_stage(s), sb + (2 * wave + m) * 1024, 16, 0, 0);
 #pragma unroll
         for (int m = 0; m < 2; ++m)
             __builtin_amdgcn_global_load_lds(bsrc[m] + (size_t)s * kBigK, sb + kBigGuA + (2 * wave + m) * 1024, 16, 0, 0);

@@ -55,7 +55,9 @@ __global__ __launch_bounds__(256) void k_gate_up_rt(ExpertLaunch L) {
     const int nkb = H / kKB;
     const int kb0 = (wave * nkb) / kWaves, kb1 = ((wave + 1) * nkb) / kWaves;
 
-    const size_t roff = (size_t)(r0 + c) * H + g * 32;
+    const int gl = __builtin_amdgcn_readfirstlane(u.e.gu_layout);
+    const size_t roff = gu_piece_off(gl, H, r0 + c, 0, g);
+    const size_t kw = gu_kstep(gl);  // weight bytes between k-blocks
     const uint8_t* pg = u.e.w_gate + roff;
     const uint8_t* pu = u.e.w_up + roff;
     const float* sg = u.e.s_gate + (size_t)(r0 / u.e.gate_rb) * ((H + u.e.gate_cb - 1) / u.e.gate_cb);
@@ -84,10 +86,10 @@ __global__ __launch_bounds__(256) void k_gate_up_rt(ExpertLaunch L) {
     for (int s = 0; s < D; ++s) {
         const int k = kb0 + s;
         if (k < kb1) {
-            wb[s][0] = ld16(pg + k * kKB);
-            wb[s][1] = ld16(pg + k * kKB + 16);
-            wb[s][2] = ld16(pu + k * kKB);
-            wb[s][3] = ld16(pu + k * kKB + 16);
+            wb[s][0] = ld16(pg + k * kw);
+            wb[s][1] = ld16(pg + k * kw + 16);
+            wb[s][2] = ld16(pu + k * kw);
+            wb[s][3] = ld16(pu + k * kw + 16);
             if (MAXT == 1) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) xb[s][j] = ld16(xp[0] + k * kKB + 8 * j);
@@ -756,7 +758,7 @@ __global__ void k_generic_gate_up(cx_expert_desc e, const void* x, int in_dtype,
     float up = 0.f, gate = 0.f;
     for (int k = 0; k < e.hidden; ++k) {
         const float xv = act_val(x, (size_t)t * e.hidden + k, in_dtype);
-        const size_t wi = (size_t)r * e.hidden + k;
+        const size_t wi = gu_elem_off(e.gu_layout, e.hidden, r, k);
         const float wu = fp8_val(e.w_up[wi]) * e.s_up[(r / e.up_rb) * ncu + k / e.up_cb];
         const float wg = fp8_val(e.w_gate[wi]) * e.s_gate[(r / e.gate_rb) * ncg + k / e.gate_cb];
         up = __fadd_rn(up, __fmul_rn(wu, xv));

@@ -48,6 +48,7 @@ __device__ __forceinline__ bool resolve_unit(const ExpertLaunch& L, int item, in
         u->e.gate_rb = r.gate_rb;
         u->e.down_rb = r.down_rb;
         u->e.up_cb = u->e.gate_cb = u->e.down_cb = kKB;  // grouped layers are 128-column blocks
+        u->e.gu_layout = r.gu_layout;
 #pragma unroll
         for (int q = 0; q < 4; ++q) u->tok[q] = r.tok[q];
     } else {
@@ -99,10 +100,12 @@ inline size_t gate_up_lds_bytes(int ksa, int maxt, int np_lds, int hidden) {
 // spread one expert's rows over twice the CUs.
 // gate_up_tile_unit: the tile of a work unit the caller has resolved (u.np
 // > 0); gate_up_tile resolves it from the launch first.
-template <int NKB, int D, int MAXT, bool F16, bool XLDS, int KS, bool SINGLE, int KSA = KS,
-          int TR = kTileRows, bool PARTIAL = false>
-__device__ __forceinline__ void gate_up_tile_unit(const ExpertLaunch& L, int tile, const Unit& u,
-                                                  unsigned char* lds, int kpart = 0) {
+// GL: the weights' layout (gu_layout), a compile-time choice per instance so
+// that each keeps constant k-block strides.
+template <int NKB, int D, int MAXT, bool F16, bool XLDS, int KS, bool SINGLE, int KSA, int TR,
+          bool PARTIAL, int GL>
+__device__ __forceinline__ void gate_up_tile_body(const ExpertLaunch& L, int tile, const Unit& u,
+                                                  unsigned char* lds, int kpart) {
     static_assert(!PARTIAL || (SINGLE && MAXT == 1), "k-part sums: single mode, <= 16 tokens");
     typedef Mma<F16> M;
     typedef typename M::V V;
@@ -118,7 +121,8 @@ __device__ __forceinline__ void gate_up_tile_unit(const ExpertLaunch& L, int til
 
     // TR = 8: lanes c and c + 8 read the same row (one fetch per wave
     // instruction); MFMA rows 8..15 are discarded
-    const size_t roff = (size_t)(r0 + (c & (TR - 1))) * H + (size_t)kb0 * kKB + g * 32;
+    constexpr int KW = GL == CX_LAYOUT_TILE16 ? 2048 : kKB;  // weight bytes between k-blocks
+    const size_t roff = gu_piece_off(GL, H, r0 + (c & (TR - 1)), kb0, g);
     const uint8_t* pg = u.e.w_gate + roff;
     const uint8_t* pu = u.e.w_up + roff;
     // integer division runs on the VALU: pin the (uniform) results to SGPRs
@@ -175,10 +179,10 @@ __device__ __forceinline__ void gate_up_tile_unit(const ExpertLaunch& L, int til
     u32x4 wb[D][4];
 #pragma unroll
     for (int s = 0; s < D && s < NKB; ++s) {
-        wb[s][0] = ld16(pg + s * kKB);
-        wb[s][1] = ld16(pg + s * kKB + 16);
-        wb[s][2] = ld16(pu + s * kKB);
-        wb[s][3] = ld16(pu + s * kKB + 16);
+        wb[s][0] = ld16(pg + s * KW);
+        wb[s][1] = ld16(pg + s * KW + 16);
+        wb[s][2] = ld16(pu + s * KW);
+        wb[s][3] = ld16(pu + s * KW + 16);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -235,10 +239,10 @@ __device__ __forceinline__ void gate_up_tile_unit(const ExpertLaunch& L, int til
             // refill this stage right after its last use, D stages ahead
             __builtin_amdgcn_sched_barrier(0);
             const int kn = k + D;
-            wb[s][0] = ld16(pg + kn * kKB);
-            wb[s][1] = ld16(pg + kn * kKB + 16);
-            wb[s][2] = ld16(pu + kn * kKB);
-            wb[s][3] = ld16(pu + kn * kKB + 16);
+            wb[s][0] = ld16(pg + kn * KW);
+            wb[s][1] = ld16(pg + kn * KW + 16);
+            wb[s][2] = ld16(pu + kn * KW);
+            wb[s][3] = ld16(pu + kn * KW + 16);
             if (XRING) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) xb[s][j] = ld16(xp[0] + kn * kKB + 8 * j);
@@ -296,6 +300,16 @@ __device__ __forceinline__ void gate_up_tile_unit(const ExpertLaunch& L, int til
                 *reinterpret_cast<float4*>(L.h_f32 + p * I + row) = float4{hv[0], hv[1], hv[2], hv[3]};
         }
     }
+}
+
+template <int NKB, int D, int MAXT, bool F16, bool XLDS, int KS, bool SINGLE, int KSA = KS,
+          int TR = kTileRows, bool PARTIAL = false>
+__device__ __forceinline__ void gate_up_tile_unit(const ExpertLaunch& L, int tile, const Unit& u,
+                                                  unsigned char* lds, int kpart = 0) {
+    if (u.e.gu_layout == CX_LAYOUT_TILE16)
+        gate_up_tile_body<NKB, D, MAXT, F16, XLDS, KS, SINGLE, KSA, TR, PARTIAL, CX_LAYOUT_TILE16>(L, tile, u, lds, kpart);
+    else
+        gate_up_tile_body<NKB, D, MAXT, F16, XLDS, KS, SINGLE, KSA, TR, PARTIAL, CX_LAYOUT_ROWS>(L, tile, u, lds, kpart);
 }
 
 template <int NKB, int D, int MAXT, bool F16, bool XLDS, int KS, bool SINGLE, int KSA = KS,

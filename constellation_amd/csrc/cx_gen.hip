@@ -144,7 +144,8 @@ __global__ void k_gen_normal(uint64_t base, uint64_t count, float std_dev, int d
 
 // One workgroup per scale block: pass 1 finds amax, pass 2 quantises.
 __global__ __launch_bounds__(256) void k_gen_fp8(uint64_t base, int rows, int cols, int rb,
-                                                 int cb, float std_dev, uint8_t* q, float* scale) {
+                                                 int cb, float std_dev, uint8_t* q, float* scale,
+                                                 int layout) {
     const int ncb = (cols + cb - 1) / cb;
     const int br = blockIdx.x / ncb, bc = blockIdx.x - br * ncb;
     const int r0 = br * rb, c0 = bc * cb;
@@ -169,7 +170,7 @@ __global__ __launch_bounds__(256) void k_gen_fp8(uint64_t base, int rows, int co
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
         const int r = r0 + i / nc, c = c0 + i % nc;
         const float v = __fmul_rn(std_dev, gen_normal(base, (uint64_t)r * cols + c));
-        q[(size_t)r * cols + c] = fp8_encode(__fdiv_rn(v, s));
+        q[gu_elem_off(layout, cols, r, c)] = fp8_encode(__fdiv_rn(v, s));
     }
 }
 
@@ -183,7 +184,44 @@ __global__ void k_canonicalize(uint8_t* p, uint64_t n) {
     }
 }
 
+// Row-major fp8 bytes -> CX_LAYOUT_TILE16, with the 0x7F/0xFF
+// canonicalisation of k_canonicalize: one thread per 32-byte piece.
+__global__ __launch_bounds__(256) void k_tile16_fp8(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                    int rows, int cols) {
+    const int ppr = cols / 32;  // pieces per row
+    const uint64_t n = (uint64_t)rows * ppr;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const int r = (int)(i / ppr), p = (int)(i - (uint64_t)r * ppr);
+        typedef uint32_t w4 __attribute__((ext_vector_type(4)));
+        const uint8_t* a = src + (size_t)r * cols + (size_t)p * 32;
+        w4 v[2] = {*reinterpret_cast<const w4*>(a), *reinterpret_cast<const w4*>(a + 16)};
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint32_t x = v[h][w];
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    if (((x >> (8 * b)) & 0x7Fu) == 0x7Fu) x -= 1u << (8 * b);
+                v[h][w] = x;
+            }
+        uint8_t* d = dst + gu_piece_off(CX_LAYOUT_TILE16, cols, r, p >> 2, p & 3);
+        *reinterpret_cast<w4*>(d) = v[0];
+        *reinterpret_cast<w4*>(d + 16) = v[1];
+    }
+}
+
 }  // namespace
+
+hipError_t launch_tile16_fp8(const uint8_t* src, uint8_t* dst, int rows, int cols, hipStream_t s) {
+    if (!gu_tile16_ok(rows, cols)) return hipErrorInvalidValue;
+    uint64_t blocks = ((uint64_t)rows * (cols / 32) + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks == 0) return hipSuccess;
+    cx_launch(k_tile16_fp8, dim3((unsigned)blocks), dim3(256), 0, s, src, dst, rows, cols);
+    return hipGetLastError();
+}
 
 hipError_t launch_gen_normal(uint64_t seed, uint64_t stream_id, uint64_t count, float std_dev,
                              int dtype, void* out, hipStream_t s) {
@@ -197,11 +235,12 @@ hipError_t launch_gen_normal(uint64_t seed, uint64_t stream_id, uint64_t count, 
 }
 
 hipError_t launch_gen_fp8(uint64_t seed, uint64_t stream_id, int rows, int cols, int rb, int cb,
-                          float std_dev, uint8_t* q, float* scale, hipStream_t s) {
+                          float std_dev, uint8_t* q, float* scale, hipStream_t s, int layout) {
+    if (layout == CX_LAYOUT_TILE16 && !gu_tile16_ok(rows, cols)) return hipErrorInvalidValue;
     const uint64_t base = mix64_host(seed, stream_id);
     const int nblk = ((rows + rb - 1) / rb) * ((cols + cb - 1) / cb);
     cx_launch(k_gen_fp8, dim3(nblk), dim3(256), 0, s, base, rows, cols, rb, cb, std_dev,
-                       q, scale);
+                       q, scale, layout);
     return hipGetLastError();
 }
 

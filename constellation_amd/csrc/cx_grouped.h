@@ -147,7 +147,7 @@ __device__ __forceinline__ void grp_stream(Issue&& issue, Publish&& publish, Com
 // ---------------------------------------------------------------------------
 // gate/up.  NKB = hidden / 128 k-blocks (<= 64), NT = 16-pair column tiles
 // of this item (1..4, a compile-time branch per item).
-template <int NKB, int NT, bool F16, bool SINGLE>
+template <int NKB, int NT, bool F16, bool SINGLE, int GL>
 __device__ __forceinline__ void grp_gate_up_item(const ExpertLaunch& L, const Unit& u, int tile,
                                                  unsigned char* lds) {
     typedef Mma<F16> M;
@@ -162,7 +162,8 @@ __device__ __forceinline__ void grp_gate_up_item(const ExpertLaunch& L, const Un
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int g = lane >> 4, c = lane & 15;
     const int r0 = tile * kGuGrpRows + wave * kTileRows;
-    const size_t roff = (size_t)(r0 + c) * H + g * 32;
+    constexpr int KW = GL == CX_LAYOUT_TILE16 ? 2048 : kKB;  // weight bytes between k-blocks
+    const size_t roff = gu_piece_off(GL, H, r0 + c, 0, g);
     const uint8_t* pg = u.e.w_gate + roff;
     const uint8_t* pu = u.e.w_up + roff;
     const int rbg = __builtin_amdgcn_readfirstlane(r0 / u.e.gate_rb);
@@ -196,10 +197,10 @@ __device__ __forceinline__ void grp_gate_up_item(const ExpertLaunch& L, const Un
         accu[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     auto issue = [&](int k, int s) {
-        wb[s][0] = ld16(pg + (size_t)k * kKB);
-        wb[s][1] = ld16(pg + (size_t)k * kKB + 16);
-        wb[s][2] = ld16(pu + (size_t)k * kKB);
-        wb[s][3] = ld16(pu + (size_t)k * kKB + 16);
+        wb[s][0] = ld16(pg + (size_t)k * KW);
+        wb[s][1] = ld16(pg + (size_t)k * KW + 16);
+        wb[s][2] = ld16(pu + (size_t)k * KW);
+        wb[s][3] = ld16(pu + (size_t)k * KW + 16);
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt) xr[s][tt] = ld8(xs[tt] + (size_t)k * kKB);
     };
@@ -275,7 +276,7 @@ constexpr int kGuChunk = 14;
 constexpr size_t kGuChunkBytes = (size_t)kGuChunk * kActBlk;  // 56 KB
 constexpr size_t grp_gu_c1_lds() { return 2 * kGuChunkBytes; }
 
-template <int NKB, bool F16, bool SINGLE, int D = kGuGrpD>
+template <int NKB, bool F16, bool SINGLE, int GL, int D = kGuGrpD>
 __device__ __forceinline__ void grp_gate_up_item_c1(const ExpertLaunch& L, const Unit& u, int tile,
                                                     unsigned char* lds) {
     typedef Mma<F16> M;
@@ -287,7 +288,8 @@ __device__ __forceinline__ void grp_gate_up_item_c1(const ExpertLaunch& L, const
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const int g = lane >> 4, c = lane & 15;
     const int r0 = tile * kGuGrpRows + wave * kTileRows;
-    const size_t roff = (size_t)(r0 + c) * H + g * 32;
+    constexpr int KW = GL == CX_LAYOUT_TILE16 ? 2048 : kKB;  // weight bytes between k-blocks
+    const size_t roff = gu_piece_off(GL, H, r0 + c, 0, g);
     const uint8_t* pg = u.e.w_gate + roff;
     const uint8_t* pu = u.e.w_up + roff;
     const int rbg = __builtin_amdgcn_readfirstlane(r0 / u.e.gate_rb);
@@ -328,7 +330,7 @@ __device__ __forceinline__ void grp_gate_up_item_c1(const ExpertLaunch& L, const
     const uint8_t* pub = pu;
     auto issue = [&](int k, int kb) {
         const int st = k % D;
-        const size_t o = (size_t)(k - kb) * kKB;
+        const size_t o = (size_t)(k - kb) * KW;
         wb[st][0] = ld16(pgb + o);
         wb[st][1] = ld16(pgb + o + 16);
         wb[st][2] = ld16(pub + o);
@@ -354,8 +356,8 @@ __device__ __forceinline__ void grp_gate_up_item_c1(const ExpertLaunch& L, const
     for (int ch = 0; ch < NCH; ++ch) {
         const unsigned char* src = lds + (size_t)(ch & 1) * kGuChunkBytes + lane * 16;
         if (ch > 0) {
-            pgb += (size_t)kGuChunk * kKB;
-            pub += (size_t)kGuChunk * kKB;
+            pgb += (size_t)kGuChunk * KW;
+            pub += (size_t)kGuChunk * KW;
             asm volatile("" : "+v"(pgb), "+v"(pub));
         }
 #pragma unroll
@@ -417,22 +419,29 @@ __device__ __forceinline__ void grp_gate_up_item_c1(const ExpertLaunch& L, const
 }
 
 // C1: one-tile items take the chunked path (needs grp_gu_c1_lds() of LDS).
+template <int NKB, bool F16, bool SINGLE, bool C1, int GL>
+__device__ __forceinline__ void grp_gate_up_unit(const ExpertLaunch& L, const Unit& u, int tile,
+                                                 unsigned char* lds) {
+    const int nt = (u.np + kTileTok - 1) / kTileTok;  // uniform: one branch per item
+    if constexpr (C1) {
+        if (nt == 1) {
+            grp_gate_up_item_c1<NKB, F16, SINGLE, GL>(L, u, tile, lds);
+            return;
+        }
+    }
+    if (nt == 1) grp_gate_up_item<NKB, 1, F16, SINGLE, GL>(L, u, tile, lds);
+    else if (nt == 2) grp_gate_up_item<NKB, 2, F16, SINGLE, GL>(L, u, tile, lds);
+    else if (nt == 3) grp_gate_up_item<NKB, 3, F16, SINGLE, GL>(L, u, tile, lds);
+    else grp_gate_up_item<NKB, 4, F16, SINGLE, GL>(L, u, tile, lds);
+}
+
 template <int NKB, bool F16, bool SINGLE, bool C1 = false>
 __device__ __forceinline__ void grp_gate_up_tile(const ExpertLaunch& L, int tile, int item,
                                                  unsigned char* lds) {
     Unit u;
     if (!resolve_unit<SINGLE>(L, item, kGrpPairs, &u)) return;
-    const int nt = (u.np + kTileTok - 1) / kTileTok;  // uniform: one branch per item
-    if constexpr (C1) {
-        if (nt == 1) {
-            grp_gate_up_item_c1<NKB, F16, SINGLE>(L, u, tile, lds);
-            return;
-        }
-    }
-    if (nt == 1) grp_gate_up_item<NKB, 1, F16, SINGLE>(L, u, tile, lds);
-    else if (nt == 2) grp_gate_up_item<NKB, 2, F16, SINGLE>(L, u, tile, lds);
-    else if (nt == 3) grp_gate_up_item<NKB, 3, F16, SINGLE>(L, u, tile, lds);
-    else grp_gate_up_item<NKB, 4, F16, SINGLE>(L, u, tile, lds);
+    if (u.e.gu_layout == CX_LAYOUT_TILE16) grp_gate_up_unit<NKB, F16, SINGLE, C1, CX_LAYOUT_TILE16>(L, u, tile, lds);
+    else grp_gate_up_unit<NKB, F16, SINGLE, C1, CX_LAYOUT_ROWS>(L, u, tile, lds);
 }
 
 // ---------------------------------------------------------------------------

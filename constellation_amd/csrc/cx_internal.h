@@ -46,6 +46,29 @@ struct PlanHdr {
 };
 constexpr int kPlanHdrInts = 8;
 
+// Gate/up weight layouts (cx_expert_desc::gu_layout).  CX_LAYOUT_TILE16
+// keeps each 16-row group's k-blocks as consecutive 2 KB tiles, and inside a
+// tile the 32-byte pieces in MFMA lane order (quarter q of the 128 columns,
+// then row): the 32 bytes a lane (row r % 16, quarter q) loads for a k-block
+// sit at tile + (16 q + r % 16) * 32, and the k-blocks of a wave are 2 KB
+// apart instead of 128 bytes, so a wave's weight range is one contiguous run.
+// Byte offset of row r, columns 32 q .. 32 q + 31 of k-block kb in a matrix
+// of `cols` columns (cols % 128 == 0, rows % 16 == 0 for TILE16):
+__host__ __device__ inline size_t gu_piece_off(int layout, int cols, int r, int kb, int q) {
+    return layout == CX_LAYOUT_TILE16
+               ? ((((size_t)(r >> 4) * (size_t)(cols >> 7) + (size_t)kb) << 11) + (size_t)((q << 4) + (r & 15)) * 32)
+               : (size_t)r * (size_t)cols + (size_t)kb * 128 + (size_t)q * 32;
+}
+// Distance between consecutive k-blocks of one row.
+__host__ __device__ inline int gu_kstep(int layout) { return layout == CX_LAYOUT_TILE16 ? 2048 : 128; }
+// Byte offset of element (r, c).
+__host__ __device__ inline size_t gu_elem_off(int layout, int cols, int r, int c) {
+    return gu_piece_off(layout, cols, r, c >> 7, (c >> 5) & 3) + (size_t)(c & 31);
+}
+__host__ __device__ inline bool gu_tile16_ok(uint64_t rows, uint64_t cols) {
+    return rows % 16 == 0 && cols % 128 == 0;
+}
+
 // Flat per-item / per-slot records written by the planner, so a workgroup
 // reaches its weight pointers with one dependent load.
 struct ItemRec {
@@ -56,7 +79,7 @@ struct ItemRec {
     const float* s_gate;
     const float* s_down;
     int pb, np;            // pair range
-    int up_rb, gate_rb, down_rb, pad;
+    int up_rb, gate_rb, down_rb, gu_layout;
     int tok[4];            // tokens of the item's first (up to) 4 pairs
 };
 
@@ -261,8 +284,14 @@ hipError_t launch_gate_up_sel(const ExpertLaunch& L, const RouteArgs& r, const d
 
 // Upload helpers / generator.
 hipError_t launch_canonicalize_fp8(uint8_t* p, uint64_t n, hipStream_t s);
+// layout: where element (r, c) goes (gu_elem_off); CX_LAYOUT_TILE16 needs
+// gu_tile16_ok(rows, cols).
 hipError_t launch_gen_fp8(uint64_t seed, uint64_t stream_id, int rows, int cols, int rb,
-                          int cb, float std_dev, uint8_t* q, float* scale, hipStream_t s);
+                          int cb, float std_dev, uint8_t* q, float* scale, hipStream_t s,
+                          int layout = CX_LAYOUT_ROWS);
+// Row-major fp8 `src` -> CX_LAYOUT_TILE16 `dst` (distinct buffers), with the
+// 0x7F/0xFF canonicalisation of launch_canonicalize_fp8.
+hipError_t launch_tile16_fp8(const uint8_t* src, uint8_t* dst, int rows, int cols, hipStream_t s);
 hipError_t launch_gen_normal(uint64_t seed, uint64_t stream_id, uint64_t count,
                              float std_dev, int dtype, void* out, hipStream_t s);
 

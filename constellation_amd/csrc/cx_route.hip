@@ -809,7 +809,7 @@ __device__ __forceinline__ void plan_build(const int32_t* __restrict__ ids, cons
         const int t2 = np > 2 ? P.pair_token[pb + 2] : 0;
         const int t3 = np > 3 ? P.pair_token[pb + 3] : 0;
         P.item_rec[i] = ItemRec{e.w_up, e.w_gate, e.w_down, e.s_up, e.s_gate, e.s_down, pb, np,
-                                e.up_rb, e.gate_rb, e.down_rb, 0, {t0, t1, t2, t3}};
+                                e.up_rb, e.gate_rb, e.down_rb, e.gu_layout, {t0, t1, t2, t3}};
     }
     if (tid == 0) {
         const int shared_items = shared ? (n_tokens + item_cap - 1) / item_cap : 0;
@@ -969,7 +969,7 @@ __device__ __forceinline__ void plan_build_staged(const int32_t* __restrict__ id
                 const int t2 = np > 2 ? P.pair_token[q0 + 2] : 0;
                 const int t3 = np > 3 ? P.pair_token[q0 + 3] : 0;
                 P.item_rec[it] = ItemRec{e.w_up, e.w_gate, e.w_down, e.s_up, e.s_gate, e.s_down,
-                                         q0, np, e.up_rb, e.gate_rb, e.down_rb, 0, {t0, t1, t2, t3}};
+                                         q0, np, e.up_rb, e.gate_rb, e.down_rb, e.gu_layout, {t0, t1, t2, t3}};
             }
             ++it;
         }
@@ -1116,7 +1116,7 @@ __device__ __forceinline__ void dec_plan_core(DecPlanLds& S, int T, int K, int E
             }
         }
         P.item_rec[slot] = ItemRec{d.w_up, d.w_gate, d.w_down, d.s_up, d.s_gate, d.s_down, first, cnt,
-                                   d.up_rb, d.gate_rb, d.down_rb, 0, {tk0, tk1, tk2, tk3}};
+                                   d.up_rb, d.gate_rb, d.down_rb, d.gu_layout, {tk0, tk1, tk2, tk3}};
     }
     if (shared) {
         if (tid == 0) {
@@ -1129,7 +1129,7 @@ __device__ __forceinline__ void dec_plan_core(DecPlanLds& S, int T, int K, int E
             P.item_pair_begin[ts] = 0;
             P.item_pair_count[ts] = T;
             P.item_rec[ts] = ItemRec{d.w_up, d.w_gate, d.w_down, d.s_up, d.s_gate, d.s_down, 0, T,
-                                     d.up_rb, d.gate_rb, d.down_rb, 0, {0, 1, 2, 3}};
+                                     d.up_rb, d.gate_rb, d.down_rb, d.gu_layout, {0, 1, 2, 3}};
         }
         if (tid < T) {
             P.pair_token[tid] = tid;
@@ -1633,7 +1633,7 @@ __device__ __forceinline__ void dec_sel_plan(const ExpertLaunch& L, const SelArg
         const cx_expert_desc d = L.table[routed ? isel : S.n_experts];  // entry E: the shared expert
         L.plan.item_rec[routed ? rank : K] =
             ItemRec{d.w_up, d.w_gate, d.w_down, d.s_up, d.s_gate, d.s_down, routed ? s0 + rank : 0, 1,
-                    d.up_rb, d.gate_rb, d.down_rb, 0, {0, 0, 0, 0}};
+                    d.up_rb, d.gate_rb, d.down_rb, d.gu_layout, {0, 0, 0, 0}};
     }
     if (lane == 0) {
         PlanHdr h{};

@@ -959,6 +959,51 @@ int cx_upload_matrix(int device, const uint8_t* host_weight, uint64_t rows, uint
     return CX_OK;
 }
 
+int cx_upload_matrix_tiled(int device, const uint8_t* host_weight, uint64_t rows, uint64_t cols,
+                           const float* host_scale, uint64_t scale_count, uint8_t** dev_weight,
+                           float** dev_scale) {
+    if (!dev_weight || !dev_scale) return fail(CX_EINVAL, "NULL output pointer");
+    *dev_weight = nullptr;
+    *dev_scale = nullptr;
+    if (!host_weight || !host_scale || rows == 0 || cols == 0 || scale_count == 0)
+        return fail(CX_EINVAL, "empty matrix or scales");
+    if (!gu_tile16_ok(rows, cols) || rows > (1u << 30) || cols > (1u << 30))
+        return fail(CX_EINVAL, "tiled upload needs rows %% 16 == 0 and cols %% 128 == 0 (got %llu x %llu)",
+                    (unsigned long long)rows, (unsigned long long)cols);
+    int rc = set_device(device);
+    if (rc) return rc;
+    const size_t wbytes = rows * cols, sbytes = scale_count * 4;
+    void *pw = nullptr, *ps = nullptr, *stage = nullptr;
+    if ((rc = arena_alloc(device, wbytes, &pw))) return rc;
+    if ((rc = arena_alloc(device, sbytes, &ps))) {
+        arena_free(device, pw, false);
+        return rc;
+    }
+    // the wire bytes land in a second arena block first (freed before
+    // returning), then one kernel re-tiles them into the expert's block
+    if ((rc = arena_alloc(device, wbytes, &stage))) {
+        arena_free(device, pw, false);
+        arena_free(device, ps, false);
+        return rc;
+    }
+    hipStream_t s = upload_stream(device);
+    hipError_t e = hipMemcpyAsync(stage, host_weight, wbytes, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(ps, host_scale, sbytes, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = launch_tile16_fp8(static_cast<const uint8_t*>(stage), static_cast<uint8_t*>(pw), (int)rows,
+                              (int)cols, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    arena_free(device, stage, false);
+    if (e != hipSuccess) {
+        arena_free(device, pw, false);
+        arena_free(device, ps, false);
+        return fail(CX_EHIP, "tiled upload failed: %s", hipGetErrorString(e));
+    }
+    *dev_weight = static_cast<uint8_t*>(pw);
+    *dev_scale = static_cast<float*>(ps);
+    return CX_OK;
+}
+
 int cx_free_device(int device, void* dev_ptr) {
     if (device >= 64) return fail(CX_EINVAL, "bad device");
     if (device >= 0) return arena_free(device, dev_ptr);
@@ -1431,11 +1476,13 @@ int cx_gen_expert(int device, uint64_t seed, uint64_t stream_base, int hidden, i
         }
     }
     hipStream_t s = upload_stream(device);
+    // up and gate in 16-row tiles when the shape allows (as the node's upload stores them)
+    const int gl = gu_tile16_ok(inter, hidden) ? CX_LAYOUT_TILE16 : CX_LAYOUT_ROWS;
     hipError_t e = launch_gen_fp8(seed, stream_base + 0, inter, hidden, block, block, std_dev,
-                                  static_cast<uint8_t*>(p[0]), static_cast<float*>(p[1]), s);
+                                  static_cast<uint8_t*>(p[0]), static_cast<float*>(p[1]), s, gl);
     if (e == hipSuccess)
         e = launch_gen_fp8(seed, stream_base + 1, inter, hidden, block, block, std_dev,
-                           static_cast<uint8_t*>(p[2]), static_cast<float*>(p[3]), s);
+                           static_cast<uint8_t*>(p[2]), static_cast<float*>(p[3]), s, gl);
     if (e == hipSuccess)
         e = launch_gen_fp8(seed, stream_base + 2, hidden, inter, block, block, std_dev,
                            static_cast<uint8_t*>(p[4]), static_cast<float*>(p[5]), s);
@@ -1453,6 +1500,7 @@ int cx_gen_expert(int device, uint64_t seed, uint64_t stream_base, int hidden, i
     out->hidden = hidden;
     out->inter = inter;
     out->up_rb = out->up_cb = out->gate_rb = out->gate_cb = out->down_rb = out->down_cb = block;
+    out->gu_layout = gl;
     return CX_OK;
 }
 

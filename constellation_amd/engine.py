@@ -57,6 +57,26 @@ def arena_stats(device: int = 0) -> tuple[int, int]:
     return u.value, r.value
 
 
+LAYOUT_ROWS, LAYOUT_TILE16 = 0, 1  # cx_expert_desc::gu_layout
+
+
+def untile16(a: np.ndarray) -> np.ndarray:
+    """CX_LAYOUT_TILE16 bytes of a [rows, cols] matrix (as read back from the
+    device, in a [rows, cols] array) in row-major order: tiles of 16 rows x
+    128 columns in row-group, then column order; inside a tile, the 32 bytes
+    of row r, columns 32q .. 32q + 31 at (16q + r) * 32."""
+    rows, cols = a.shape
+    t = a.reshape(rows // 16, cols // 128, 4, 16, 32)   # [row group][k-block][quarter][row][32 B]
+    return np.ascontiguousarray(t.transpose(0, 3, 1, 2, 4)).reshape(rows, cols)
+
+
+def tile16(a: np.ndarray) -> np.ndarray:
+    """Row-major [rows, cols] bytes in CX_LAYOUT_TILE16 order (untile16's inverse)."""
+    rows, cols = a.shape
+    t = np.ascontiguousarray(a).reshape(rows // 16, 16, cols // 128, 4, 32)
+    return np.ascontiguousarray(t.transpose(0, 2, 3, 1, 4)).reshape(rows, cols)
+
+
 class Expert:
     """A device-resident fp8 expert living in the library's HBM arena."""
 
@@ -67,26 +87,35 @@ class Expert:
 
     @classmethod
     def upload(cls, device: int, w_up, s_up, w_gate, s_gate, w_down, s_down, *,
-               row_block: int = 128, col_block: int = 128) -> "Expert":
-        """Upload host fp8 bytes + fp32 scale_inv (the UploadExpertAmdV2 path)."""
+               row_block: int = 128, col_block: int = 128, tiled: Optional[bool] = None) -> "Expert":
+        """Upload host fp8 bytes + fp32 scale_inv (the UploadExpertAmdV2 path).
+        Up and gate are re-tiled on the device (CX_LAYOUT_TILE16) when the
+        shape allows, as the node's upload does; tiled=False keeps them
+        row-major."""
         w_up, w_gate, w_down = (np.ascontiguousarray(a, np.uint8) for a in (w_up, w_gate, w_down))
         s_up, s_gate, s_down = (np.ascontiguousarray(a, np.float32) for a in (s_up, s_gate, s_down))
         inter, hidden = w_up.shape
         if w_gate.shape != (inter, hidden) or w_down.shape != (hidden, inter):
             raise ValueError("expert shapes must be up/gate [I,H] and down [H,I]")
+        ok = inter % 16 == 0 and hidden % 128 == 0
+        if tiled is None:
+            tiled = ok
+        elif tiled and not ok:
+            raise ValueError("tiled gate/up needs inter % 16 == 0 and hidden % 128 == 0")
         ptrs = []
         try:
-            for w, s in ((w_up, s_up), (w_gate, s_gate), (w_down, s_down)):
+            for w, s, t in ((w_up, s_up, tiled), (w_gate, s_gate, tiled), (w_down, s_down, False)):
                 dw, ds = C.c_void_p(), C.c_void_p()
-                check(lib().cx_upload_matrix(device, w.ctypes.data, w.shape[0], w.shape[1],
-                                             s.ctypes.data, s.size, C.byref(dw), C.byref(ds)))
+                up = lib().cx_upload_matrix_tiled if t else lib().cx_upload_matrix
+                check(up(device, w.ctypes.data, w.shape[0], w.shape[1], s.ctypes.data, s.size,
+                         C.byref(dw), C.byref(ds)))
                 ptrs += [dw.value, ds.value]
         except Exception:
             for p in ptrs:
                 lib().cx_free_device(device, p)
             raise
         d = ExpertDesc(*ptrs, hidden, inter, row_block, col_block, row_block, col_block,
-                       row_block, col_block)
+                       row_block, col_block, LAYOUT_TILE16 if tiled else LAYOUT_ROWS)
         return cls(device, d)
 
     @classmethod
@@ -120,6 +149,8 @@ class Expert:
                 shape = ((rows + rb - 1) // rb, (cols + cb - 1) // cb)
             a = np.empty(shape, dt)
             _hip_d2h(a, ptr)
+            if name in ("w_up", "w_gate") and self.desc.gu_layout == LAYOUT_TILE16:
+                a = untile16(a)
             out[name] = a
         out.update(hidden=H, inter=I, rb=self.desc.up_rb, cb=self.desc.up_cb)
         return out

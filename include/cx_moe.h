@@ -88,6 +88,22 @@ CX_API int cx_upload_matrix(int device,
                      const float* host_scale, uint64_t scale_count,
                      uint8_t** dev_weight, float** dev_scale);
 
+/* The same upload with the weight re-tiled on the device for the gate/up
+ * kernels (CX_LAYOUT_TILE16: 2 KB tiles of 16 rows x 128 columns, the tiles
+ * of a 16-row group in column order; inside a tile the 32 bytes of row r,
+ * columns 32q..32q+31 at (16q + r) * 32), so that each wave's weight range
+ * is contiguous in HBM.  The wire bytes, the scales and the result of every
+ * kernel are unchanged; rows % 16 == 0 and cols % 128 == 0 are required.
+ * Mark the descriptor's gu_layout CX_LAYOUT_TILE16 for an expert whose up
+ * and gate came this way.  No counterpart in the reference: its CUDA
+ * upload (backend/cuda/backend_cuda_v2.cc:94-145) keeps all three matrices
+ * row-major; this library's UploadExpertAmdV2 calls this entry for w_up and
+ * w_gate when the shape allows. */
+CX_API int cx_upload_matrix_tiled(int device,
+                     const uint8_t* host_weight, uint64_t rows, uint64_t cols,
+                     const float* host_scale, uint64_t scale_count,
+                     uint8_t** dev_weight, float** dev_scale);
+
 /* Release one arena sub-allocation made by this library (weight or scale).
  * device < 0 searches every device's arena for the pointer (the reference's
  * FreeDeviceBuffer takes no device either).  NULL is a no-op.  Like
@@ -103,7 +119,12 @@ CX_API int cx_arena_stats(int device, uint64_t* used_bytes, uint64_t* reserved_b
 /* Device-resident expert, the plain-pointer image of ExpertDeviceStorageV2
  * (expert_node_v2/expert_format_v2.h:170-237):
  *   up, gate: [inter, hidden];  down: [hidden, inter]  (HF nn.Linear [out,in]).
- * *_rb / *_cb are the row/col block sizes of each matrix's scale grid. */
+ * *_rb / *_cb are the row/col block sizes of each matrix's scale grid.
+ * gu_layout: how w_up and w_gate sit in HBM, CX_LAYOUT_ROWS (row-major, the
+ * wire order) or CX_LAYOUT_TILE16 (cx_upload_matrix_tiled; the scales stay
+ * row-major).  w_down is always row-major. */
+#define CX_LAYOUT_ROWS 0
+#define CX_LAYOUT_TILE16 1
 typedef struct cx_expert_desc {
     const uint8_t* w_up;   const float* s_up;
     const uint8_t* w_gate; const float* s_gate;
@@ -111,6 +132,8 @@ typedef struct cx_expert_desc {
     int32_t hidden;        /* 7168 for DeepSeek-V3 */
     int32_t inter;         /* 2048 */
     int32_t up_rb, up_cb, gate_rb, gate_cb, down_rb, down_cb;
+    int32_t gu_layout;     /* CX_LAYOUT_ROWS or CX_LAYOUT_TILE16 */
+    int32_t reserved[3];   /* zero */
 } cx_expert_desc;
 
 /* ---- per-worker context -------------------------------------------------- */
@@ -315,12 +338,14 @@ CX_API int cx_gen_fp8_matrix(cx_ctx* ctx, uint64_t seed, uint64_t stream_id,
 CX_API int cx_gen_normal(cx_ctx* ctx, uint64_t seed, uint64_t stream_id,
                   uint64_t count, float std_dev, int dtype, void* dev_out,
                   void* stream);
-/* Allocate (arena) and generate a whole expert (hidden x inter, blocks). */
+/* Allocate (arena) and generate a whole expert (hidden x inter, blocks).
+ * Up and gate are written in CX_LAYOUT_TILE16 when inter % 16 == 0 and
+ * hidden % 128 == 0 (out->gu_layout says which); the values are the same. */
 CX_API int cx_gen_expert(int device, uint64_t seed, uint64_t stream_base,
                   int hidden, int inter, int block, float std_dev,
                   cx_expert_desc* out);
 /* Free the six arena buffers of an expert made by cx_gen_expert or by
- * cx_upload_matrix calls, and zero the descriptor. */
+ * cx_upload_matrix / cx_upload_matrix_tiled calls, and zero the descriptor. */
 CX_API int cx_free_expert(int device, cx_expert_desc* expert);
 
 #ifdef __cplusplus
