@@ -20,6 +20,9 @@
 //                          kernel's shape, by tiles per workgroup and occupancy
 //   cx_kbench fused1       one expert, one token: one launch split over inter (w_down
 //                          as k-panels) + a reduce launch, against the two launches
+//   cx_kbench decode-layout  one-token gate/up and down launch shapes streamed bare
+//                          in natural rows and in 16-row x 128-column tiles, and
+//                          k_gate_up_kpart / k_gate_up_t reading either gate/up layout
 //   cx_kbench rates        per-CU rates the LDS-ring kernels are built on, in shader
 //                          clocks (s_memtime): ds_read_b128 bytes per clock, bf16
 //                          MFMA and fp8 -> 16-bit convert issue intervals, and
@@ -84,7 +87,7 @@ __global__ void k_fill_f32(float* p, size_t n, float v) {
 struct Pool {
     std::vector<uint8_t*> chunks;
     std::vector<cx_expert_desc> d;
-    explicit Pool(bool spread) {
+    explicit Pool(bool spread, int gu_layout = CX_LAYOUT_ROWS) {
         const int per_chunk = (int)(kChunk / kExpert);
         const int n_chunks = spread ? 24 : 1;
         const size_t bytes = spread ? kChunk : kExpert * 48;
@@ -111,6 +114,7 @@ struct Pool {
             q.hidden = kH;
             q.inter = kI;
             q.up_rb = q.up_cb = q.gate_rb = q.gate_cb = q.down_rb = q.down_cb = 128;
+            q.gu_layout = gu_layout;
         }
         KB_CHECK(hipDeviceSynchronize());
     }
@@ -128,7 +132,7 @@ T* dev_copy(const std::vector<T>& v) {
 }
 
 ItemRec item_of(const cx_expert_desc& q, int pb, int np) {
-    return ItemRec{q.w_up, q.w_gate, q.w_down, q.s_up, q.s_gate, q.s_down, pb, np, 128, 128, 128, 0, {0, 0, 0, 0}};
+    return ItemRec{q.w_up, q.w_gate, q.w_down, q.s_up, q.s_gate, q.s_down, pb, np, 128, 128, 128, q.gu_layout, {0, 0, 0, 0}};
 }
 
 // Average single-launch time (us) of `n` launches issued back to back, each
@@ -1072,6 +1076,188 @@ int cmd_fused1(int iters) {
     return 0;
 }
 
+// ---------------------------------------------------------------------------
+// Decode weight layouts.  Bare streams (no compute) of the one-token launch
+// shapes, each reading the same bytes per lane in two orders: natural rows
+// (lane = row c of a 16-row group, quarter g of a 128-byte k-block: 16 rows
+// 128 B apart per k-step of 7168 or 2048 B) and tile-contiguous (the 16
+// rows x 128 columns of one k-step are one 2 KB tile, lane l at 32 l: what
+// CX_LAYOUT_TILE16 stores for gate/up).
+template <bool TILED>
+__device__ __forceinline__ size_t gu_bare_off(int rt, int kb, int lane, int cols) {
+    return TILED ? ((size_t)rt * (cols / kKB) + kb) * 2048 + lane * 32
+                 : (size_t)(rt * 16 + (lane & 15)) * cols + (size_t)kb * kKB + (lane >> 4) * 32;
+}
+
+// gate/up k-part shape (k_gate_up_kpart): 128 row tiles x 2 k-parts = 256
+// workgroups of 8 waves, 7 active x 4 k-blocks of gate and up each.
+template <bool TILED>
+__global__ __launch_bounds__(512) void k_bare_kpart_gu(cx_expert_desc e, uint32_t* sink) {
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    if (wave >= 7) return;
+    const int rt = blockIdx.x >> 1, kb0 = (blockIdx.x & 1) * 28 + wave * 4;
+    u32x4 v[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const size_t off = gu_bare_off<TILED>(rt, kb0 + k, lane, kH);
+        v[4 * k + 0] = ld16(e.w_gate + off);
+        v[4 * k + 1] = ld16(e.w_gate + off + 16);
+        v[4 * k + 2] = ld16(e.w_up + off);
+        v[4 * k + 3] = ld16(e.w_up + off + 16);
+    }
+    uint32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc ^= v[i][0] + v[i][1] * 3u + v[i][2] * 5u + v[i][3] * 7u;
+    if (acc == 0x12345678u) sink[threadIdx.x] = acc;
+}
+
+// down k-split shape (k_down_ks): 224 workgroups of 8 waves = 2 groups of 16
+// rows x 4 k ranges of 4 k-blocks.
+template <bool TILED>
+__global__ __launch_bounds__(512) void k_bare_ks_dn(cx_expert_desc e, uint32_t* sink) {
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int rg = blockIdx.x * 2 + (wave >> 2), kr = wave & 3;
+    u32x4 v[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const size_t off = gu_bare_off<TILED>(rg, kr * 4 + k, lane, kI);
+        v[2 * k] = ld16(e.w_down + off);
+        v[2 * k + 1] = ld16(e.w_down + off + 16);
+    }
+    uint32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc ^= v[i][0] + v[i][1] * 3u + v[i][2] * 5u + v[i][3] * 7u;
+    if (acc == 0x12345678u) sink[threadIdx.x] = acc;
+}
+
+// one-token routed gate/up shape (k_gate_up_t, k_gate_up_sel): grid 128 row
+// tiles x 8 experts, 4 waves x 14 k-blocks, a 4-deep register ring.
+template <bool TILED>
+__global__ __launch_bounds__(256) void k_bare_b1_gu(GuPtrs P, uint32_t* sink) {
+    constexpr int NKB = 14, D = 4;
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int rt = blockIdx.x, kb0 = wave * NKB;
+    const uint8_t* pg = P.gate[blockIdx.y];
+    const uint8_t* pu = P.up[blockIdx.y];
+    u32x4 wb[D][4];
+    uint32_t acc = 0;
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+        const size_t off = gu_bare_off<TILED>(rt, kb0 + s, lane, kH);
+        wb[s][0] = ld16(pg + off);
+        wb[s][1] = ld16(pg + off + 16);
+        wb[s][2] = ld16(pu + off);
+        wb[s][3] = ld16(pu + off + 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < NKB; ++k) {
+        const int s = k % D;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc ^= wb[s][q][0] + wb[s][q][1] * 3u + wb[s][q][2] * 5u + wb[s][q][3] * 7u;
+        __builtin_amdgcn_sched_barrier(0);
+        if (k + D < NKB) {
+            const size_t off = gu_bare_off<TILED>(rt, kb0 + k + D, lane, kH);
+            wb[s][0] = ld16(pg + off);
+            wb[s][1] = ld16(pg + off + 16);
+            wb[s][2] = ld16(pu + off);
+            wb[s][3] = ld16(pu + off + 16);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (acc == 0x12345678u) sink[threadIdx.x] = acc;
+}
+
+int cmd_decode_layout(int iters) {
+    Pool pool(true);
+    const int n = std::min<int>(64, (int)pool.d.size());
+    std::printf("decode-layout: one token, experts spread over 24 x 2 GiB (%d rotated for one expert)\n", n);
+    uint32_t* sink = nullptr;
+    KB_CHECK(hipMalloc(&sink, 4096));
+    std::mt19937 rng(13);
+    std::vector<GuPtrs> sets(16);
+    for (auto& st : sets)
+        for (int j = 0; j < 8; ++j) {
+            const cx_expert_desc& q = pool.d[rng() % pool.d.size()];
+            st.gate[j] = q.w_gate;
+            st.up[j] = q.w_up;
+        }
+    auto one = [&](int i) { return pool.d[((i % n) * 17) % pool.d.size()]; };
+    const int lds = max_lds();
+    uint16_t *x = nullptr, *y = nullptr;
+    float* gu = nullptr;
+    KB_CHECK(hipMalloc(&x, kH * 2));
+    KB_CHECK(hipMemset(x, 0x3c, kH * 2));
+    KB_CHECK(hipMalloc(&y, kH * 2));
+    KB_CHECK(hipMalloc(&gu, 2 * 2 * kI * 4));
+    // the library's kernels read the layout from the descriptor; the bytes are
+    // synthetic, so one buffer serves both readings
+    auto expert_launch = [&](int i, int layout) {
+        ExpertLaunch L{};
+        L.single = one(i);
+        L.single.gu_layout = layout;
+        L.n_tokens = 1;
+        L.hidden = kH;
+        L.inter = kI;
+        L.maxt = 1;
+        L.x = x;
+        L.in_dtype = CX_DTYPE_BF16;
+        L.y = y;
+        L.out_dtype = CX_DTYPE_BF16;
+        L.np_lds = 1;
+        L.max_lds = lds;
+        L.gu_part = gu;
+        L.gu_kparts = 2;
+        return L;
+    };
+    DecodePlans dp_rows(pool, 16, 3);
+    for (auto& q : pool.d) q.gu_layout = CX_LAYOUT_TILE16;
+    DecodePlans dp_tiled(pool, 16, 3);
+    cx_expert_desc* table = dev_copy(pool.d);
+    const double b1_gu = 16.0 * kMat, kpart_gu = 2.0 * kMat;
+    const double t_bytes = 8.0 * (2 * kMat + 2 * 16 * 56 * 4) + kH * 2;
+    for (int rep = 0; rep < 3; ++rep) {
+        std::printf(" pass %d\n", rep + 1);
+        report("bare one-token routed gate/up shape, natural rows", time_launches(iters, [&](int i) {
+                   cx_launch(k_bare_b1_gu<false>, dim3(128, 8), dim3(256), 0u, (hipStream_t)0, sets[i % 16], sink);
+               }), b1_gu);
+        report("bare one-token routed gate/up shape, tile-contiguous", time_launches(iters, [&](int i) {
+                   cx_launch(k_bare_b1_gu<true>, dim3(128, 8), dim3(256), 0u, (hipStream_t)0, sets[i % 16], sink);
+               }), b1_gu);
+        report("bare gate/up k-part shape, natural rows", time_launches(iters, [&](int i) {
+                   cx_launch(k_bare_kpart_gu<false>, dim3(256), dim3(512), 0u, (hipStream_t)0, one(i), sink);
+               }), kpart_gu);
+        report("bare gate/up k-part shape, tile-contiguous", time_launches(iters, [&](int i) {
+                   cx_launch(k_bare_kpart_gu<true>, dim3(256), dim3(512), 0u, (hipStream_t)0, one(i), sink);
+               }), kpart_gu);
+        report("bare down k-split shape, natural rows", time_launches(iters, [&](int i) {
+                   cx_launch(k_bare_ks_dn<false>, dim3(224), dim3(512), 0u, (hipStream_t)0, one(i), sink);
+               }), 1.0 * kMat);
+        report("bare down k-split shape, tile-contiguous", time_launches(iters, [&](int i) {
+                   cx_launch(k_bare_ks_dn<true>, dim3(224), dim3(512), 0u, (hipStream_t)0, one(i), sink);
+               }), 1.0 * kMat);
+        for (int layout = 0; layout < 2; ++layout) {
+            const char* tag = layout ? "CX_LAYOUT_TILE16" : "CX_LAYOUT_ROWS";
+            char what[96];
+            std::snprintf(what, sizeof what, "k_gate_up_kpart, %s", tag);
+            report(what, time_launches(iters, [&](int i) {
+                       KB_CHECK(launch_gate_up_kpart(expert_launch(i, layout), 0));
+                   }), kpart_gu + 2 * 16 * 56 * 4 + kH * 2);
+            std::snprintf(what, sizeof what, "k_gate_up_t (8 routed experts), %s", tag);
+            const DecodePlans& dp = layout ? dp_tiled : dp_rows;
+            report(what, time_launches(iters, [&](int i) {
+                       KB_CHECK(launch_gate_up(dp.launch(i, table, lds), 0));
+                   }), t_bytes);
+        }
+    }
+    (void)hipFree(table);
+    (void)hipFree(x);
+    (void)hipFree(y);
+    (void)hipFree(gu);
+    (void)hipFree(sink);
+    return 0;
+}
+
 int cmd_rates(int iters) {
     const int cus = n_cu();
     const int n = 2000 * std::max(1, iters / 30);
@@ -1141,6 +1327,8 @@ int main(int argc, char** argv) {
     if (!std::strcmp(cmd, "grouped-down")) return cmd_grouped_down(std::min(iters, 12));
     if (!std::strcmp(cmd, "rates")) return cmd_rates(iters);
     if (!std::strcmp(cmd, "fused1")) return cmd_fused1(iters);
-    std::fprintf(stderr, "usage: cx_kbench layout|decode-down|placement|decode-balance|grouped|rates|fused1 [launches]\n");
+    if (!std::strcmp(cmd, "decode-layout")) return cmd_decode_layout(iters);
+    std::fprintf(stderr, "usage: cx_kbench layout|decode-down|placement|decode-balance|grouped|grouped-down|"
+                         "rates|fused1|decode-layout [launches]\n");
     return 2;
 }
