@@ -498,70 +498,98 @@ __global__ __launch_bounds__(512) void k_gate_up_kpart(ExpertLaunch L) {
 constexpr int kDownKsRows = 4;   // tokens of the split-K down launch
 constexpr int kDownKsGroups = 2;  // 16-row groups per workgroup
 
-inline size_t down_ks_lds(int nkbw) {
+constexpr size_t down_ks_lds(int nkbw) {
     return (size_t)4 * 2 * kDownKsRows * ((size_t)nkbw * kKB * 2 + 16) + (size_t)4 * kDownKsGroups * 64 * 16;
 }
 
+// The down k-split in pieces (the measured one-launch form of this expert,
+// cx_kbench one-launch, issues the weights long before the part sums exist
+// and runs the same pieces):
+//  * down_ks_parts: this wave's half of its k range's part sums (global loads)
+//  * down_ks_weights: this wave's 16 rows x NKBW k-blocks of Wd (all in flight)
+//  * down_ks_h: h = silu(g0 + g1) * (u0 + u1) into LDS
+//  * down_ks_mma: MFMA on the weights (fp8, or converted ahead), k-order sum, store
+// Workgroup `blk` covers row groups 2 blk, 2 blk + 1 (wave >> 2) x 4 k ranges (wave & 3).
 template <int NKBW>
-__global__ __launch_bounds__(512) void k_down_ks(ExpertLaunch L) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char dk_lds[];
-    constexpr int KW = NKBW * kKB;      // k per range
-    constexpr size_t HS = KW * 2 + 16;  // LDS row stride (bytes) of one h plane
-    constexpr int NI = KW / 4;          // 4-k items per token and range
-    constexpr int ITEMS = (NI + 127) / 128;
-    const int H = L.hidden, I = L.inter, np = L.n_tokens;
-    const cx_expert_desc& e = L.single;
+struct DownKsParts {
+    static constexpr int KW = NKBW * kKB;  // k per range
+    static constexpr int NI = KW / 4;      // 4-k items per token and range
+    static constexpr int ITEMS = (NI + 127) / 128;
+    float4 g0[kDownKsRows][ITEMS], g1[kDownKsRows][ITEMS], u0[kDownKsRows][ITEMS], u1[kDownKsRows][ITEMS];
+};
+
+template <int NKBW>
+__device__ __forceinline__ void down_ks_parts(const ExpertLaunch& L, DownKsParts<NKBW>& P) {
+    typedef DownKsParts<NKBW> DP;
+    const int I = L.inter, np = L.n_tokens;
     const int wave = wave_id(), lane = threadIdx.x & 63;
-    const int rg = wave >> 2, kq = wave & 3;
-    const int g = lane >> 4, c = lane & 15;
-    const int r0 = (blockIdx.x * kDownKsGroups + rg) * kTileRows;
-    const int kb0 = kq * NKBW;
-    unsigned char* hw = dk_lds + (size_t)kq * (2 * kDownKsRows * HS);
-    f32x4* red = reinterpret_cast<f32x4*>(dk_lds + 4 * (2 * kDownKsRows * HS));  // [8][64]
-    // 1) part sums of this wave's half of the k range (older than the weight
-    //    loads, so waiting for them leaves the weights in flight)
+    const int rg = wave >> 2, kb0 = (wave & 3) * NKBW;
     const size_t T = (size_t)np;
     const float* gp = L.gu_part + (size_t)kb0 * kKB;
-    float4 pg0[kDownKsRows][ITEMS], pg1[kDownKsRows][ITEMS], pu0[kDownKsRows][ITEMS], pu1[kDownKsRows][ITEMS];
 #pragma unroll
     for (int q = 0; q < kDownKsRows; ++q) {
         if (q < np) {
 #pragma unroll
-            for (int it = 0; it < ITEMS; ++it) {
+            for (int it = 0; it < DP::ITEMS; ++it) {
                 const int i = it * 128 + rg * 64 + lane;
-                if (NI % 128 != 0 && i >= NI) continue;
+                if (DP::NI % 128 != 0 && i >= DP::NI) continue;
                 const size_t k4 = (size_t)i * 4;
-                pg0[q][it] = *reinterpret_cast<const float4*>(gp + ((0 * 2 + 0) * T + q) * I + k4);
-                pg1[q][it] = *reinterpret_cast<const float4*>(gp + ((1 * 2 + 0) * T + q) * I + k4);
-                pu0[q][it] = *reinterpret_cast<const float4*>(gp + ((0 * 2 + 1) * T + q) * I + k4);
-                pu1[q][it] = *reinterpret_cast<const float4*>(gp + ((1 * 2 + 1) * T + q) * I + k4);
+                P.g0[q][it] = *reinterpret_cast<const float4*>(gp + ((0 * 2 + 0) * T + q) * I + k4);
+                P.g1[q][it] = *reinterpret_cast<const float4*>(gp + ((1 * 2 + 0) * T + q) * I + k4);
+                P.u0[q][it] = *reinterpret_cast<const float4*>(gp + ((0 * 2 + 1) * T + q) * I + k4);
+                P.u1[q][it] = *reinterpret_cast<const float4*>(gp + ((1 * 2 + 1) * T + q) * I + k4);
             }
         }
     }
-    __builtin_amdgcn_sched_barrier(0);
-    // 2) this wave's 16 rows x KW of Wd, all in flight
-    const uint8_t* pd = e.w_down + (size_t)(r0 + c) * I + (size_t)kb0 * kKB + g * 32;
-    u32x4 wb[NKBW][2];
+}
+
+template <int NKBW>
+__device__ __forceinline__ const uint8_t* down_ks_row(const ExpertLaunch& L, int blk) {
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int r0 = (blk * kDownKsGroups + (wave >> 2)) * kTileRows;
+    return L.single.w_down + (size_t)(r0 + (lane & 15)) * L.inter + (size_t)(wave & 3) * NKBW * kKB +
+           (lane >> 4) * 32;
+}
+
+template <int NKBW>
+__device__ __forceinline__ void down_ks_weights(const uint8_t* pd, u32x4 (&wb)[NKBW][2]) {
 #pragma unroll
     for (int k = 0; k < NKBW; ++k) {
         wb[k][0] = ld16(pd + k * kKB);
         wb[k][1] = ld16(pd + k * kKB + 16);
     }
-    __builtin_amdgcn_sched_barrier(0);
+}
+
+// This wave's down scales (scalar loads, held in SGPRs).
+template <int NKBW>
+__device__ __forceinline__ void down_ks_scales(const ExpertLaunch& L, int blk, float (&scd)[NKBW]) {
+    const cx_expert_desc& e = L.single;
+    const int wave = wave_id();
+    const int r0 = (blk * kDownKsGroups + (wave >> 2)) * kTileRows;
     const int rbd = __builtin_amdgcn_readfirstlane(r0 / e.down_rb);
-    const float* sd = e.s_down + (size_t)rbd * (I / kKB) + kb0;
-    float scd[NKBW];
+    const float* sd = e.s_down + (size_t)rbd * (L.inter / kKB) + (wave & 3) * NKBW;
 #pragma unroll
     for (int k = 0; k < NKBW; ++k) scd[k] = ldsc(sd + k);
-    // 3) h = silu(gate) * up, bf16 hi + lo, into the k range's LDS slice
+}
+
+// h = silu(g0 + g1) * (u0 + u1), bf16 hi + lo, into the k range's LDS slice,
+// then a workgroup barrier.
+template <int NKBW>
+__device__ __forceinline__ void down_ks_h(const ExpertLaunch& L, const DownKsParts<NKBW>& P, unsigned char* lds) {
+    typedef DownKsParts<NKBW> DP;
+    constexpr size_t HS = DP::KW * 2 + 16;  // LDS row stride (bytes) of one h plane
+    const int np = L.n_tokens;
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int rg = wave >> 2, kq = wave & 3;
+    unsigned char* hw = lds + (size_t)kq * (2 * kDownKsRows * HS);
 #pragma unroll
     for (int q = 0; q < kDownKsRows; ++q) {
         if (q < np) {
 #pragma unroll
-            for (int it = 0; it < ITEMS; ++it) {
+            for (int it = 0; it < DP::ITEMS; ++it) {
                 const int i = it * 128 + rg * 64 + lane;
-                if (NI % 128 != 0 && i >= NI) continue;
-                const float4 a = pg0[q][it], b = pg1[q][it], u = pu0[q][it], v = pu1[q][it];
+                if (DP::NI % 128 != 0 && i >= DP::NI) continue;
+                const float4 a = P.g0[q][it], b = P.g1[q][it], u = P.u0[q][it], v = P.u1[q][it];
                 const float gs[4] = {a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w};
                 const float us[4] = {u.x + v.x, u.y + v.y, u.z + v.z, u.w + v.w};
                 uint32_t hi[4], lo[4];
@@ -579,7 +607,23 @@ __global__ __launch_bounds__(512) void k_down_ks(ExpertLaunch L) {
         }
     }
     __syncthreads();
-    // 4) MFMA steps over this wave's rows and k range
+}
+
+// MFMA steps over this wave's rows and k range (step(k, hb): the product of
+// k-block k with the h fragment hb), the 4 partial tiles of a row group
+// summed in LDS in k order, and the store.
+template <int NKBW, class Step>
+__device__ __forceinline__ void down_ks_mma(const ExpertLaunch& L, int blk, const float (&scd)[NKBW], unsigned char* lds,
+                                            Step step) {
+    typedef DownKsParts<NKBW> DP;
+    constexpr size_t HS = DP::KW * 2 + 16;
+    const int H = L.hidden, np = L.n_tokens;
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int rg = wave >> 2, kq = wave & 3;
+    const int g = lane >> 4, c = lane & 15;
+    const int r0 = (blk * kDownKsGroups + rg) * kTileRows;
+    unsigned char* hw = lds + (size_t)kq * (2 * kDownKsRows * HS);
+    f32x4* red = reinterpret_cast<f32x4*>(lds + 4 * (2 * kDownKsRows * HS));  // [8][64]
     const size_t hrow = (size_t)min(c, np - 1);
     const unsigned char* lh = hw + hrow * HS + g * 64;
     const unsigned char* ll = hw + (kDownKsRows + hrow) * HS + g * 64;
@@ -592,7 +636,7 @@ __global__ __launch_bounds__(512) void k_down_ks(ExpertLaunch L) {
             hb[j] = *reinterpret_cast<const u32x4*>(lh + k * (kKB * 2) + 16 * j);
             hb[4 + j] = *reinterpret_cast<const u32x4*>(ll + k * (kKB * 2) + 16 * j);
         }
-        acc += scd[k] * down_step(wb[k], hb);
+        acc += scd[k] * step(k, hb);
     }
     red[wave * 64 + lane] = acc;
     __syncthreads();
@@ -601,6 +645,23 @@ __global__ __launch_bounds__(512) void k_down_ks(ExpertLaunch L) {
         const f32x4 sum = ((rr[lane] + rr[64 + lane]) + rr[128 + lane]) + rr[192 + lane];
         store_out4(L.y, L.y_f32, (size_t)c * H + r0 + 4 * g, sum, L.out_dtype);
     }
+}
+
+template <int NKBW>
+__global__ __launch_bounds__(512) void k_down_ks(ExpertLaunch L) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char dk_lds[];
+    // part sums first: older than the weight loads, so waiting for them
+    // leaves the weights in flight
+    DownKsParts<NKBW> P;
+    down_ks_parts<NKBW>(L, P);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 wb[NKBW][2];
+    down_ks_weights<NKBW>(down_ks_row<NKBW>(L, blockIdx.x), wb);
+    __builtin_amdgcn_sched_barrier(0);
+    float scd[NKBW];
+    down_ks_scales<NKBW>(L, blockIdx.x, scd);
+    down_ks_h<NKBW>(L, P, dk_lds);
+    down_ks_mma<NKBW>(L, blockIdx.x, scd, dk_lds, [&](int k, const u32x4(&hb)[8]) { return down_step(wb[k], hb); });
 }
 
 // ---------------------------------------------------------------------------

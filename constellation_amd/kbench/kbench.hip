@@ -23,6 +23,9 @@
 //   cx_kbench decode-layout  one-token gate/up and down launch shapes streamed bare
 //                          in natural rows and in 16-row x 128-column tiles, and
 //                          k_gate_up_kpart / k_gate_up_t reading either gate/up layout
+//   cx_kbench one-launch   one expert, one token: k_expert_one (gate/up, grid barrier,
+//                          down in one launch) against the two launches, and the
+//                          grid barrier's own cost
 //   cx_kbench rates        per-CU rates the LDS-ring kernels are built on, in shader
 //                          clocks (s_memtime): ds_read_b128 bytes per clock, bf16
 //                          MFMA and fp8 -> 16-bit convert issue intervals, and
@@ -1258,6 +1261,621 @@ int cmd_decode_layout(int iters) {
     return 0;
 }
 
+// ---------------------------------------------------------------------------
+// The measured one-launch form of one expert at 1..4 tokens (not the library's
+// path: the library runs k_gate_up_kpart + k_down_ks).  Its pieces: the bf16
+// down step on weights converted ahead, part sums read at the coherence point,
+// the kernel with its grid barrier, and its launcher.
+// down_step on weights already converted to bf16 (wc[i] = cvt of the i-th
+// 8-byte pair of w: w[0][0..1], w[0][2..3], w[1][0..1], w[1][2..3]): the same
+// MFMAs in the same order, so the same result.
+typedef typename Mma<false>::V DnV;
+__device__ __forceinline__ void down_cvt(const u32x4 w[2], DnV wc[4]) {
+    typedef Mma<false> M;
+    wc[0] = M::cvt(w[0][0], w[0][1]);
+    wc[1] = M::cvt(w[0][2], w[0][3]);
+    wc[2] = M::cvt(w[1][0], w[1][1]);
+    wc[3] = M::cvt(w[1][2], w[1][3]);
+}
+
+__device__ __forceinline__ f32x4 down_step_cv(const DnV wc[4], const u32x4 hb[8]) {
+    typedef Mma<false> M;
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 t = M::mma(wc[0], M::bits(hb[0]), zero);
+    t = M::mma(wc[0], M::bits(hb[4]), t);
+    t = M::mma(wc[1], M::bits(hb[1]), t);
+    t = M::mma(wc[1], M::bits(hb[5]), t);
+    t = M::mma(wc[2], M::bits(hb[2]), t);
+    t = M::mma(wc[2], M::bits(hb[6]), t);
+    t = M::mma(wc[3], M::bits(hb[3]), t);
+    t = M::mma(wc[3], M::bits(hb[7]), t);
+    return t;
+}
+
+// down_ks_parts for part sums written by other workgroups of the same launch
+// (k_expert_one): read at the device coherence point (sc1), past any stale
+// copy an XCD's L2 may hold from an earlier launch.
+constexpr int kCpolSc1 = 16;  // buffer cache policy: device scope (sc1)
+
+template <int NKBW>
+__device__ __forceinline__ void down_ks_parts_sc1(const ExpertLaunch& L, DownKsParts<NKBW>& P) {
+    typedef DownKsParts<NKBW> DP;
+    const int I = L.inter, np = L.n_tokens;
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int rg = wave >> 2, kb0 = (wave & 3) * NKBW;
+    const size_t T = (size_t)np;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(L.gu_part, (uint32_t)(4 * T * I * sizeof(float)));
+    auto part = [&](size_t idx) -> float4 {  // idx: float index from gp
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rs, (uint32_t)(((size_t)kb0 * kKB + idx) * 4), 0, kCpolSc1));
+    };
+#pragma unroll
+    for (int q = 0; q < kDownKsRows; ++q) {
+        if (q < np) {
+#pragma unroll
+            for (int it = 0; it < DP::ITEMS; ++it) {
+                const int i = it * 128 + rg * 64 + lane;
+                if (DP::NI % 128 != 0 && i >= DP::NI) continue;
+                const size_t k4 = (size_t)i * 4;
+                P.g0[q][it] = part(((0 * 2 + 0) * T + q) * I + k4);
+                P.g1[q][it] = part(((1 * 2 + 0) * T + q) * I + k4);
+                P.u0[q][it] = part(((0 * 2 + 1) * T + q) * I + k4);
+                P.u1[q][it] = part(((1 * 2 + 1) * T + q) * I + k4);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// One expert at 1..4 tokens in one launch (hidden 7168, inter 2048): the
+// gate/up k-part tiles and the down k-split above, in one workgroup per CU,
+// with every wave's weights for both phases issued at the start (44 MB in
+// flight over 256 CUs), so the down weights stream while the gate/up is still
+// arriving and computing.  Between the phases a grid barrier: workgroup b
+// writes the part sums of gate/up tile b >> 1, k-part b & 1; after the
+// barrier workgroups b < 224 finalise h for their k ranges and run the down
+// of rows 32 b .. 32 b + 31.  The arithmetic is that of k_gate_up_kpart +
+// k_down_ks, operation for operation, so the results are bit-identical.
+// Roles of the 8 waves:
+//  * waves 0..6 stream and multiply 4 k-blocks of the tile's gate and up rows
+//    (16 KB), then their down task's 16 rows x 4 k-blocks (8 KB) into
+//    registers; a workgroup barrier between the two issues puts all of a
+//    CU's gate/up requests ahead of its down requests;
+//  * wave 0 sums the waves' tiles, stores the part sums and arrives at the
+//    grid barrier.  An arrival waits for every memory operation of its wave
+//    (vmcnt counts loads and stores alike), so wave 0 holds no down weights:
+//    its 8 register loads read the token row (L2 hits), and wave 7 loads
+//    wave 0's down task beside its own and hands it over in LDS, converted to
+//    bf16, while wave 0 waits at the barrier (waves 1..7 convert their own
+//    then too, so only the MFMAs are left after it);
+//  * wave 7 has no gate/up rows (28 k-blocks per k-part = 7 x 4) and stages
+//    no token rows.
+// Residency: 96 KB of LDS per workgroup admits one per CU, and the launch
+// has kOneWg <= CUs workgroups (expert_one_ok), so all are resident at once.
+constexpr int kOneErrBarrier = 32;     // *err bit: a barrier wait gave up
+constexpr int kOneWg = 256;           // 128 gate/up row tiles x 2 k-parts
+constexpr int kOneNkb = 4;            // gate/up k-blocks per wave
+constexpr int kOneKsa = 7;            // gate/up waves per workgroup (x 4 k-blocks = 28 = one k-part)
+constexpr uint32_t kOneLds = 96 * 1024;
+constexpr uint32_t kOneW0Lds = 80 * 1024;  // wave 0's down weights as bf16 (16 KB), past the gate/up and down regions
+constexpr unsigned kOneSpin = 1u << 18;    // polls before a barrier wait gives up (~0.1-0.3 s)
+constexpr size_t kOneBarBytes = 8192;      // the barrier counters' allocation (17 lines of 256 B used)
+
+// Grid barrier, a two-level arrival tree on monotonic counters (one 256-byte
+// line each): workgroup b arrives at group counter g = b & 7 (32 arrivals per
+// launch), the last arrival of a group at the top counter (8 per launch), and
+// the top's last arrival stores the release value in each group's release
+// word, where that group's workgroups poll.  Every counter starts at zero
+// (zeroed once at allocation) and grows by a power of two per launch, so it
+// wraps cleanly and nothing is reset; the release value is the group
+// count at the end of the launch, 32 n in launch n, the same in every group,
+// and a workgroup whose arrival returned `old` waits for (old & -32) + 32.
+// Relaxed atomics only, with no cache maintenance: the data that crosses the
+// barrier (the part sums) is written and read at the device coherence point
+// (sc1), and thread 0 arrives only after its wave's stores have completed
+// (s_waitcnt vmcnt(0)).  Measured at one token: device-scope atomics on one
+// address serialise, and 256 arrivals within a microsecond took 1-2 us each
+// (the tree: 0.3-0.4); an acquire in the polling loop (an L2 invalidate per
+// poll) made the barrier alone 25 us, release + acquire around it 5 us.  A
+// workgroup with no work after the barrier only arrives (wait == false).  The
+// wait is bounded: after kOneSpin polls the workgroup sets kOneErrBarrier in
+// *err and goes on.
+constexpr int kOneGroups = 8, kOneLine = 64;  // groups; words per 256-byte line
+__device__ __forceinline__ void one_grid_barrier(unsigned* bar, bool wait, int* err) {
+    static_assert(kOneWg % kOneGroups == 0 && ((kOneWg / kOneGroups) & (kOneWg / kOneGroups - 1)) == 0,
+                  "equal power-of-two groups");
+    constexpr unsigned per = kOneWg / kOneGroups;
+    if (threadIdx.x == 0) {
+        const int grp = blockIdx.x % kOneGroups;
+        unsigned* gcount = bar + kOneLine * (1 + grp);
+        unsigned* rel = bar + kOneLine * (1 + kOneGroups + grp);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        vm_wait<0>();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        const unsigned old = __hip_atomic_fetch_add(gcount, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned target = (old & ~(per - 1)) + per;
+        bool released = false;
+        if (old + 1 == target) {
+            const unsigned top = __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((top & (kOneGroups - 1)) == kOneGroups - 1) {
+#pragma unroll
+                for (int r = 0; r < kOneGroups; ++r)
+                    __hip_atomic_store(bar + kOneLine * (1 + kOneGroups + r), target, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                released = true;
+            }
+        }
+        if (wait && !released) {
+            unsigned n = 0;
+            while ((int)(__hip_atomic_load(rel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
+                if (++n > kOneSpin) {
+                    __hip_atomic_fetch_or(err, kOneErrBarrier, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+template <bool F16, int GL>
+__global__ __launch_bounds__(512) void k_expert_one(ExpertLaunch L, unsigned* bar, int* err) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char eo_lds[];
+    constexpr int NKB = kOneNkb, KSA = kOneKsa, NKBW = 4;
+    constexpr int KW = GL == CX_LAYOUT_TILE16 ? 2048 : kKB;  // weight bytes between k-blocks
+    typedef Mma<F16> M;
+    typedef typename M::V V;
+    const cx_expert_desc& e = L.single;
+    const int H = L.hidden, I = L.inter, np = L.n_tokens;
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const int g = lane >> 4, c = lane & 15;
+    const int tile = blockIdx.x >> 1, kpart = blockIdx.x & 1;
+    const bool active = wave < KSA;                                        // wave-uniform
+    const bool down = (int)blockIdx.x < H / (kDownKsGroups * kTileRows);  // workgroup-uniform
+    const int kb0 = (kpart * KSA + (active ? wave : 0)) * NKB;
+    const int r0 = tile * kTileRows;
+    f32x4* red = reinterpret_cast<f32x4*>(eo_lds);  // [KSA][gate, up][64]
+    unsigned char* xlds = eo_lds + gate_up_red_bytes(KSA, 1);
+    unsigned char* w0lds = eo_lds + kOneW0Lds;
+    const size_t xs = (size_t)H * 2 + 16;  // LDS row stride of the token rows
+    const uint8_t* xb = static_cast<const uint8_t*>(L.x) + lane * 32;  // stand-in address: the first token row
+
+    u32x4 wd[NKBW][2], w0[NKBW][2];  // w0: wave 0's down task, carried by wave 7
+    float scd[NKBW];                  // this wave's down scales, loaded long before they are used
+    if (down) down_ks_scales<NKBW>(L, blockIdx.x, scd);
+    if (wave == KSA) {
+        // wave 7: its own down task and wave 0's, into registers, after every
+        // gate/up request of the workgroup (first barrier); it takes no token
+        // rows, so it waits for nothing before the second.  (Register loads:
+        // LDS DMA still in flight would make every later workgroup barrier
+        // wait for all loads.)
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        down_ks_weights<NKBW>(down ? down_ks_row<NKBW>(L, blockIdx.x) : xb, wd);
+        down_ks_weights<NKBW>(down ? e.w_down + (size_t)(blockIdx.x * kDownKsGroups * kTileRows + c) * I + g * 32 : xb,
+                              w0);
+        __builtin_amdgcn_sched_barrier(0);
+        lds_dma_barrier();
+    } else {
+        // 0) the token rows to LDS by DMA (1 KB per wave instruction)
+        const int cpr = H / 512, nwc = np * cpr;
+        for (int wc = wave; wc < nwc; wc += KSA) {
+            const int q = wc / cpr, j0 = (wc - q * cpr) * 64;
+            const uint16_t* src = static_cast<const uint16_t*>(L.x) + (size_t)q * H + (size_t)(j0 + lane) * 8;
+            __builtin_amdgcn_global_load_lds(src, xlds + q * xs + j0 * 16, 16, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // 1) gate/up weights
+        const size_t roff = gu_piece_off(GL, H, r0 + c, kb0, g);
+        const uint8_t* pg = e.w_gate + roff;
+        const uint8_t* pu = e.w_up + roff;
+        u32x4 wb[NKB][4];
+#pragma unroll
+        for (int s = 0; s < NKB; ++s) {
+            wb[s][0] = ld16(pg + s * KW);
+            wb[s][1] = ld16(pg + s * KW + 16);
+            wb[s][2] = ld16(pu + s * KW);
+            wb[s][3] = ld16(pu + s * KW + 16);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();  // every wave's gate/up requests before any down request
+        __builtin_amdgcn_sched_barrier(0);
+        // 2) down weights: 8 register loads in every wave (wave 0 and the
+        //    workgroups without down work read the token row instead)
+        down_ks_weights<NKBW>(down && wave != 0 ? down_ks_row<NKBW>(L, blockIdx.x) : xb, wd);
+        __builtin_amdgcn_sched_barrier(0);
+        const int rbg = __builtin_amdgcn_readfirstlane(r0 / e.gate_rb);
+        const int rbu = __builtin_amdgcn_readfirstlane(r0 / e.up_rb);
+        const float* sg = e.s_gate + (size_t)rbg * (H / kKB) + kb0;
+        const float* su = e.s_up + (size_t)rbu * (H / kKB) + kb0;
+        float scg[NKB], scu[NKB];
+#pragma unroll
+        for (int k = 0; k < NKB; ++k) {
+            scg[k] = ldsc(sg + k);
+            scu[k] = ldsc(su + k);
+        }
+        // 3) wait for the token rows and the gate/up weights; the down loads
+        //    (younger) stay in flight
+        vm_wait<2 * NKBW>();
+        __builtin_amdgcn_sched_barrier(0);  // the weight converts stay below the wait
+        lds_dma_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        const unsigned char* xl = xlds + min(c, np - 1) * xs + ((size_t)kb0 * kKB + g * 32) * 2;
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        f32x4 accg = zero, accu = zero;
+#pragma unroll
+        for (int k = 0; k < NKB; ++k) {
+            V bx[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bx[j] = M::bits(*reinterpret_cast<const u32x4*>(xl + (k * kKB + 8 * j) * 2));
+            f32x4 tg = M::mma(M::cvt(wb[k][0][0], wb[k][0][1]), bx[0], zero);
+            tg = M::mma(M::cvt(wb[k][0][2], wb[k][0][3]), bx[1], tg);
+            tg = M::mma(M::cvt(wb[k][1][0], wb[k][1][1]), bx[2], tg);
+            tg = M::mma(M::cvt(wb[k][1][2], wb[k][1][3]), bx[3], tg);
+            f32x4 tu = M::mma(M::cvt(wb[k][2][0], wb[k][2][1]), bx[0], zero);
+            tu = M::mma(M::cvt(wb[k][2][2], wb[k][2][3]), bx[1], tu);
+            tu = M::mma(M::cvt(wb[k][3][0], wb[k][3][1]), bx[2], tu);
+            tu = M::mma(M::cvt(wb[k][3][2], wb[k][3][3]), bx[3], tu);
+            accg += scg[k] * tg;
+            accu += scu[k] * tu;
+        }
+        red[(wave * 2 + 0) * 64 + lane] = accg;
+        red[(wave * 2 + 1) * 64 + lane] = accu;
+    }
+    // an LDS-only barrier: a full __syncthreads would wait for every load in
+    // flight (wave 7's DMA writes LDS), i.e. for the down weights
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    // the down weights to bf16 while wave 0 waits at the grid barrier: waves
+    // 1..7 their own (as their loads land), wave 7 also wave 0's, handed over
+    // in LDS (published by the grid barrier's workgroup barrier)
+    DnV wcv[NKBW][4];
+    if (down && wave != 0) {
+#pragma unroll
+        for (int k = 0; k < NKBW; ++k) down_cvt(wd[k], wcv[k]);
+        if (wave == KSA) {
+#pragma unroll
+            for (int k = 0; k < NKBW; ++k) {
+                DnV c0[4];
+                down_cvt(w0[k], c0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) *reinterpret_cast<DnV*>(w0lds + (k * 4 + i) * 1024 + lane * 16) = c0[i];
+            }
+        }
+    }
+    // 4) the tile's part sums, waves summed in order (as k_gate_up_kpart),
+    //    stored at the device coherence point (sc1)
+    if (wave == 0) {
+        f32x4 G = red[lane], U = red[64 + lane];
+#pragma unroll
+        for (int w = 1; w < KSA; ++w) {
+            G += red[(w * 2 + 0) * 64 + lane];
+            U += red[(w * 2 + 1) * 64 + lane];
+        }
+        if (c < np) {
+            const size_t T = (size_t)np;
+            const int row = r0 + 4 * g;
+            const __amdgpu_buffer_rsrc_t rs = make_rsrc(L.gu_part, (uint32_t)(4 * T * I * sizeof(float)));
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, G), rs,
+                                                   (uint32_t)(((((size_t)kpart * 2 + 0) * T + c) * I + row) * 4), 0,
+                                                   kCpolSc1);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, U), rs,
+                                                   (uint32_t)(((((size_t)kpart * 2 + 1) * T + c) * I + row) * 4), 0,
+                                                   kCpolSc1);
+        }
+    }
+    one_grid_barrier(bar, down, err);
+    if (!down) return;
+    // 5) the down k-split: part sums (sc1); wave 0's weights from LDS
+    DownKsParts<NKBW> P;
+    down_ks_parts_sc1<NKBW>(L, P);
+    if (wave == 0) {
+#pragma unroll
+        for (int k = 0; k < NKBW; ++k)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wcv[k][i] = *reinterpret_cast<const DnV*>(w0lds + (k * 4 + i) * 1024 + lane * 16);
+    }
+    down_ks_h<NKBW>(L, P, eo_lds);
+    down_ks_mma<NKBW>(L, blockIdx.x, scd, eo_lds, [&](int k, const u32x4(&hb)[8]) { return down_step_cv(wcv[k], hb); });
+}
+
+bool expert_one_ok(const ExpertLaunch& L, int n_cu) {
+    return L.table == nullptr && L.n_tokens >= 1 && L.n_tokens <= kDownKsRows && L.gu_part != nullptr &&
+           L.hidden == 7168 && L.inter == 2048 && L.np_lds >= L.n_tokens && n_cu >= kOneWg &&
+           L.max_lds >= (int)kOneLds &&
+           (L.single.gu_layout == CX_LAYOUT_ROWS || L.single.gu_layout == CX_LAYOUT_TILE16);
+}
+
+static_assert(gate_up_red_bytes(kOneKsa, 1) + (size_t)kDownKsRows * (7168 * 2 + 16) <= kOneW0Lds &&
+                  down_ks_lds(4) <= kOneW0Lds && kOneW0Lds + 16 * 1024 <= kOneLds,
+              "one-launch LDS: gate/up tile + 4 token rows, then the down k-split, below wave 0's bf16 down weights");
+static_assert(kOneLds > 80 * 1024, "one workgroup per CU (160 KB of LDS)");
+
+template <bool F16, int GL>
+hipError_t go_expert_one(const ExpertLaunch& L, unsigned* bar, int* err, bool coop, hipStream_t s) {
+    auto kernel = k_expert_one<F16, GL>;
+    const dim3 grid(kOneWg), block(512);
+    if (!coop) {
+        cx_launch(kernel, grid, block, kOneLds, s, L, bar, err);
+        return hipGetLastError();
+    }
+    LaunchTimer* t = current_launch_timer();
+    hipError_t rc = hipSuccess;
+    if (t != nullptr && !t->started) {
+        if ((rc = hipEventRecord(t->start, s)) != hipSuccess) return rc;
+        t->started = true;
+    }
+    ExpertLaunch arg = L;
+    void* args[] = {&arg, &bar, &err};
+    rc = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kernel), grid, block, args, kOneLds, s);
+    if (rc == hipSuccess && t != nullptr) rc = hipEventRecord(t->stop, s);
+    return rc;
+}
+
+hipError_t launch_expert_one(const ExpertLaunch& L, unsigned* bar, int* err, int n_cu, bool coop, hipStream_t s) {
+    if (!expert_one_ok(L, n_cu)) return hipErrorInvalidValue;
+    const bool f16 = L.in_dtype == CX_DTYPE_FP16, tiled = L.single.gu_layout == CX_LAYOUT_TILE16;
+    if (f16) return tiled ? go_expert_one<true, CX_LAYOUT_TILE16>(L, bar, err, coop, s) : go_expert_one<true, CX_LAYOUT_ROWS>(L, bar, err, coop, s);
+    return tiled ? go_expert_one<false, CX_LAYOUT_TILE16>(L, bar, err, coop, s) : go_expert_one<false, CX_LAYOUT_ROWS>(L, bar, err, coop, s);
+}
+
+// ---------------------------------------------------------------------------
+// One expert, one token, in one launch (k_expert_one) against the two launches,
+// and what its grid barrier costs on its own: 256 workgroups of 8 waves with
+// 96 KB of LDS each (one per CU), empty or only crossing the barrier.
+__global__ __launch_bounds__(512) void k_one_empty(uint32_t* sink) {
+    extern __shared__ uint32_t one_lds[];
+    if (threadIdx.x == 0 && sink[0] == 0x12345678u) one_lds[0] = 1, sink[1] = one_lds[0];
+}
+
+__global__ __launch_bounds__(512) void k_one_barrier(unsigned* bar, int* err) {
+    one_grid_barrier(bar, true, err);
+}
+
+// The forms the library's barrier (one_grid_barrier: one relaxed counter, data
+// at the coherence point) replaced, for their cost alone, on a count and a
+// generation word (the last arrival resets the one and bumps the other).  MODE 0: acquire-release
+// arrival, acquire polls (an L2 invalidate per poll).  MODE 1: release
+// arrival (an L2 write-back), relaxed polls, one acquire fence after the wait.
+template <int MODE>
+__global__ __launch_bounds__(512) void k_one_barrier_form(unsigned* words, int* err) {
+    unsigned* bar = words + 64 * 20;  // [count, generation], on a line apart from the library's counters
+    if (threadIdx.x == 0) {
+        const unsigned gen = __hip_atomic_load(bar + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned old = MODE == 0 ? __hip_atomic_fetch_add(bar, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT)
+                                       : __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == gridDim.x - 1) {
+            __hip_atomic_store(bar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(bar + 1, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            unsigned n = 0;
+            while ((MODE == 0 ? __hip_atomic_load(bar + 1, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT)
+                              : __hip_atomic_load(bar + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == gen) {
+                if (++n > kOneSpin) {
+                    __hip_atomic_fetch_or(err, kOneErrBarrier, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        if (MODE == 1) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
+    if (MODE == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+// The bytes of k_expert_one streamed bare in its shape (waves 0..6: 4 k-blocks
+// of gate and up; then every wave a 16-row x 4 k-block down task, wave 7 also
+// wave 0's), no compute; then, FORM 1, the library-form tree barrier or, FORM
+// 2, one relaxed arrival counter all 256 workgroups add to (with a release
+// word on another line): the barrier's cost after a 44 MB stream.
+template <int FORM>
+__global__ __launch_bounds__(512) void k_one_bare(ExpertLaunch L, unsigned* bar, int* err, uint32_t* sink) {
+    const cx_expert_desc& e = L.single;
+    const int H = L.hidden;
+    const int wave = wave_id(), lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+    const int tile = blockIdx.x >> 1, kpart = blockIdx.x & 1;
+    const bool down = (int)blockIdx.x < H / 32;
+    const uint8_t* xb = static_cast<const uint8_t*>(L.x) + lane * 32;
+    u32x4 wb[4][4], wd[4][2], w0[4][2];
+    uint32_t acc = 0;
+    if (wave == 7) {
+        __builtin_amdgcn_s_barrier();
+        down_ks_weights<4>(down ? down_ks_row<4>(L, blockIdx.x) : xb, wd);
+        down_ks_weights<4>(down ? e.w_down + (size_t)(blockIdx.x * 32 + c) * L.inter + g * 32 : xb, w0);
+        vm_wait<0>();
+        for (int k = 0; k < 4; ++k) acc ^= w0[k][0][0] + w0[k][1][1];
+    } else {
+        const int kb0 = (kpart * 7 + wave) * 4;
+        const size_t roff = gu_piece_off(CX_LAYOUT_TILE16, H, tile * 16 + c, kb0, g);
+        for (int s = 0; s < 4; ++s) {
+            wb[s][0] = ld16(e.w_gate + roff + s * 2048);
+            wb[s][1] = ld16(e.w_gate + roff + s * 2048 + 16);
+            wb[s][2] = ld16(e.w_up + roff + s * 2048);
+            wb[s][3] = ld16(e.w_up + roff + s * 2048 + 16);
+        }
+        __builtin_amdgcn_s_barrier();
+        down_ks_weights<4>(down && wave != 0 ? down_ks_row<4>(L, blockIdx.x) : xb, wd);
+        vm_wait<0>();
+        for (int s = 0; s < 4; ++s) acc ^= wb[s][0][0] + wb[s][3][3];
+    }
+    for (int k = 0; k < 4; ++k) acc ^= wd[k][0][0] + wd[k][1][2];
+    if (acc == 0x12345678u) sink[threadIdx.x] = acc;
+    if (FORM == 1) {
+        one_grid_barrier(bar, true, err);
+    } else if (FORM == 2) {
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned* cnt = bar + 64 * 24;  // lines apart from the tree's counters
+            unsigned* rel = bar + 64 * 28;
+            const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned target = (old & ~(unsigned)(kOneWg - 1)) + (unsigned)kOneWg;
+            if (old + 1 == target) {
+                __hip_atomic_store(rel, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                unsigned n = 0;
+                while ((int)(__hip_atomic_load(rel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
+                    if (++n > kOneSpin) {
+                        __hip_atomic_fetch_or(err, kOneErrBarrier, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Round trip of one agent-scope atomic load: one wave, `n` dependent loads.
+__global__ void k_atomic_chain(unsigned* bar, int n, uint32_t* sink) {
+    unsigned v = 0;
+    for (int i = 0; i < n; ++i) v += __hip_atomic_load(bar + 1 + (v >> 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (v == 0x12345678u) sink[0] = v;
+}
+
+int cmd_one_launch(int iters) {
+    Pool pool(true);
+    const int n = std::min<int>(64, (int)pool.d.size());
+    std::printf("one-launch: one expert, one token, %d experts rotated (24 x 2 GiB chunks)\n", n);
+    const int lds = max_lds(), cus = n_cu();
+    uint16_t *x = nullptr, *y = nullptr;
+    float* gu = nullptr;
+    unsigned* bar = nullptr;
+    int* err = nullptr;
+    uint32_t* sink = nullptr;
+    KB_CHECK(hipMalloc(&x, kH * 2));
+    KB_CHECK(hipMemset(x, 0x3c, kH * 2));
+    KB_CHECK(hipMalloc(&y, kH * 2));
+    KB_CHECK(hipMalloc(&gu, 2 * 2 * kI * 4));
+    KB_CHECK(hipMalloc(&bar, kOneBarBytes));
+    KB_CHECK(hipMemset(bar, 0, kOneBarBytes));
+    KB_CHECK(hipMalloc(&err, 4));
+    KB_CHECK(hipMemset(err, 0, 4));
+    KB_CHECK(hipMalloc(&sink, 4096));
+    KB_CHECK(hipMemset(sink, 0, 4096));
+    auto launch = [&](int i, int layout) {
+        ExpertLaunch L{};
+        L.single = pool.d[((i % n) * 17) % pool.d.size()];
+        L.single.gu_layout = layout;
+        L.n_tokens = 1;
+        L.hidden = kH;
+        L.inter = kI;
+        L.maxt = 1;
+        L.x = x;
+        L.in_dtype = CX_DTYPE_BF16;
+        L.y = y;
+        L.out_dtype = CX_DTYPE_BF16;
+        L.np_lds = 1;
+        L.max_lds = lds;
+        L.gu_part = gu;
+        L.gu_kparts = 2;
+        return L;
+    };
+    if (!expert_one_ok(launch(0, CX_LAYOUT_ROWS), cus)) {
+        std::printf("  k_expert_one does not fit this device (%d CUs, %d B of LDS)\n", cus, lds);
+        return 1;
+    }
+    // the barrier alone once: every workgroup must get through it
+    cx_launch(k_one_barrier, dim3(kOneWg), dim3(512), kOneLds, (hipStream_t)0, bar, err);
+    KB_CHECK(hipDeviceSynchronize());
+    int e0 = 0;
+    KB_CHECK(hipMemcpy(&e0, err, 4, hipMemcpyDeviceToHost));
+    if (e0 != 0) {
+        std::printf("  grid barrier gave up (error bits %d): workgroups not co-resident\n", e0);
+        return 1;
+    }
+    // one launch against two: the same bits (synthetic weights, 8 experts, both layouts)
+    {
+        std::vector<uint16_t> a(kH), b(kH);
+        int same = 0, total = 0;
+        for (int layout = 0; layout < 2; ++layout)
+            for (int i = 0; i < 8; ++i) {
+                const ExpertLaunch L = launch(i, layout);
+                KB_CHECK(launch_gate_up_kpart(L, 0));
+                KB_CHECK(launch_down_ks(L, 0));
+                KB_CHECK(hipMemcpy(a.data(), y, kH * 2, hipMemcpyDeviceToHost));
+                KB_CHECK(hipMemset(y, 0, kH * 2));
+                KB_CHECK(launch_expert_one(L, bar, err, cus, i & 1, 0));
+                KB_CHECK(hipMemcpy(b.data(), y, kH * 2, hipMemcpyDeviceToHost));
+                same += a == b;
+                ++total;
+            }
+        std::printf("  k_expert_one output bit-identical to the two launches: %d of %d calls\n", same, total);
+    }
+    const double bytes = 3.0 * kMat + 3 * 16 * 56 * 4 + 2 * kH * 2;
+    for (int rep = 0; rep < 3; ++rep) {
+        std::printf(" pass %d\n", rep + 1);
+        report("empty launch, 256 workgroups x 512, 96 KB LDS", time_launches(iters, [&](int) {
+                   cx_launch(k_one_empty, dim3(kOneWg), dim3(512), kOneLds, (hipStream_t)0, sink);
+               }), 0.0);
+        report("grid barrier only (the library's: relaxed, no cache maintenance)", time_launches(iters, [&](int) {
+                   cx_launch(k_one_barrier, dim3(kOneWg), dim3(512), kOneLds, (hipStream_t)0, bar, err);
+               }), 0.0);
+        report("grid barrier only, cooperative launch", time_launches(iters, [&](int) {
+                   unsigned* b = bar;
+                   int* e = err;
+                   void* args[] = {&b, &e};
+                   LaunchTimer* t = current_launch_timer();  // null during the untimed warm-up calls
+                   if (t) KB_CHECK(hipEventRecord(t->start, 0));
+                   KB_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_one_barrier), dim3(kOneWg),
+                                                       dim3(512), args, kOneLds, 0));
+                   if (t) KB_CHECK(hipEventRecord(t->stop, 0));
+               }), 0.0);
+        report("grid barrier only: acquire polls (L2 invalidate per poll)", time_launches(iters, [&](int) {
+                   cx_launch(k_one_barrier_form<0>, dim3(kOneWg), dim3(512), kOneLds, (hipStream_t)0, bar, err);
+               }), 0.0);
+        report("grid barrier only: release arrival, one acquire after", time_launches(iters, [&](int) {
+                   cx_launch(k_one_barrier_form<1>, dim3(kOneWg), dim3(512), kOneLds, (hipStream_t)0, bar, err);
+               }), 0.0);
+        report("one wave, 1 agent-scope atomic load", time_launches(iters, [&](int) {
+                   cx_launch(k_atomic_chain, dim3(1), dim3(64), 0u, (hipStream_t)0, bar, 1, sink);
+               }), 0.0);
+        report("one wave, 101 dependent agent-scope atomic loads", time_launches(iters, [&](int) {
+                   cx_launch(k_atomic_chain, dim3(1), dim3(64), 0u, (hipStream_t)0, bar, 101, sink);
+               }), 0.0);
+        report("bare 44 MB stream in the one-launch shape (tiled gate/up)", time_launches(iters, [&](int i) {
+                   cx_launch(k_one_bare<0>, dim3(kOneWg), dim3(512), kOneLds, (hipStream_t)0, launch(i, 1), bar, err, sink);
+               }), bytes);
+        report("  then the tree barrier", time_launches(iters, [&](int i) {
+                   cx_launch(k_one_bare<1>, dim3(kOneWg), dim3(512), kOneLds, (hipStream_t)0, launch(i, 1), bar, err, sink);
+               }), bytes);
+        report("  then one arrival counter for all 256 workgroups", time_launches(iters, [&](int i) {
+                   cx_launch(k_one_bare<2>, dim3(kOneWg), dim3(512), kOneLds, (hipStream_t)0, launch(i, 1), bar, err, sink);
+               }), bytes);
+        for (int layout = 0; layout < 2; ++layout) {
+            const char* tag = layout ? "tiled gate/up" : "row-major gate/up";
+            char what[96];
+            std::snprintf(what, sizeof what, "two launches: k_gate_up_kpart + k_down_ks, %s", tag);
+            report(what, time_launches(iters, [&](int i) {
+                       const ExpertLaunch L = launch(i, layout);
+                       KB_CHECK(launch_gate_up_kpart(L, 0));
+                       KB_CHECK(launch_down_ks(L, 0));
+                   }), bytes);
+            std::snprintf(what, sizeof what, "one launch: k_expert_one, plain launch, %s", tag);
+            report(what, time_launches(iters, [&](int i) {
+                       KB_CHECK(launch_expert_one(launch(i, layout), bar, err, cus, false, 0));
+                   }), bytes);
+            std::snprintf(what, sizeof what, "one launch: k_expert_one, cooperative, %s", tag);
+            report(what, time_launches(iters, [&](int i) {
+                       KB_CHECK(launch_expert_one(launch(i, layout), bar, err, cus, true, 0));
+                   }), bytes);
+        }
+    }
+    int e = 0;
+    KB_CHECK(hipMemcpy(&e, err, 4, hipMemcpyDeviceToHost));
+    std::printf("  barrier error bits after all launches: %d\n", e);
+    (void)hipFree(x);
+    (void)hipFree(y);
+    (void)hipFree(gu);
+    (void)hipFree(bar);
+    (void)hipFree(err);
+    (void)hipFree(sink);
+    return e != 0;
+}
+
 int cmd_rates(int iters) {
     const int cus = n_cu();
     const int n = 2000 * std::max(1, iters / 30);
@@ -1328,7 +1946,8 @@ int main(int argc, char** argv) {
     if (!std::strcmp(cmd, "rates")) return cmd_rates(iters);
     if (!std::strcmp(cmd, "fused1")) return cmd_fused1(iters);
     if (!std::strcmp(cmd, "decode-layout")) return cmd_decode_layout(iters);
+    if (!std::strcmp(cmd, "one-launch")) return cmd_one_launch(iters);
     std::fprintf(stderr, "usage: cx_kbench layout|decode-down|placement|decode-balance|grouped|grouped-down|"
-                         "rates|fused1|decode-layout [launches]\n");
+                         "rates|fused1|decode-layout|one-launch [launches]\n");
     return 2;
 }
