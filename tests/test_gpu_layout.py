@@ -11,7 +11,7 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
-def _host_expert(rng, H, I):
+def _host_expert(rng, H, I, blk=128):
     def mat(r, c):
         w = rng.integers(0, 0x7E, (r, c), dtype=np.uint8)
         w ^= rng.integers(0, 2, (r, c), dtype=np.uint8) << 7          # both signs
@@ -19,15 +19,15 @@ def _host_expert(rng, H, I):
         w.ravel()[rng.integers(0, r * c, 64)] = 0xFF
         return w
     def sc(r, c):
-        return rng.uniform(5e-4, 2e-3, ((r + 127) // 128, (c + 127) // 128)).astype(np.float32)
+        return rng.uniform(5e-4, 2e-3, ((r + blk - 1) // blk, (c + blk - 1) // blk)).astype(np.float32)
     return dict(w_up=mat(I, H), s_up=sc(I, H), w_gate=mat(I, H), s_gate=sc(I, H),
                 w_down=mat(H, I), s_down=sc(H, I))
 
 
-def _upload(ex, tiled):
+def _upload(ex, tiled, blk=128):
     from constellation_amd.engine import Expert
     return Expert.upload(0, ex["w_up"], ex["s_up"], ex["w_gate"], ex["s_gate"], ex["w_down"],
-                         ex["s_down"], tiled=tiled)
+                         ex["s_down"], row_block=blk, col_block=blk, tiled=tiled)
 
 
 def _canon(w):
@@ -57,6 +57,30 @@ def test_tiled_upload_reads_back_and_runs_like_rows(gpu):
             torch.cuda.synchronize()
             assert torch.equal(yfa.view(torch.int32), yfb.view(torch.int32)), T
             assert torch.equal(ya.view(torch.int16), yb.view(torch.int16)), T
+    finally:
+        rows.free()
+        tile.free()
+
+
+@pytest.mark.parametrize("H,I,blk,Ts", [(7168, 2048, 128, (1, 5, 40)), (1024, 512, 64, (1, 4, 20))])
+def test_tiled_fp16_input_and_generic_path(gpu, H, I, blk, Ts):
+    """fp16 activations (the F16 instances of every gate/up body) at full
+    size, and 64 x 64 scale blocks, which only the generic kernels take
+    (gu_elem_off per element): tiled and row-major give the same bits."""
+    print(f"[layout] fp16 / generic H={H} I={I} blk={blk}", flush=True)
+    rng = np.random.default_rng(blk)
+    ex = _host_expert(rng, H, I, blk)
+    rows, tile = _upload(ex, False, blk), _upload(ex, True, blk)
+    try:
+        assert tile.desc.gu_layout == 1
+        for T in Ts:
+            for dt in (torch.float16, torch.bfloat16):
+                x = gpu.gen_normal(9, T, (T, H), 1.0, torch.float32).to(dt)
+                ya, yfa = gpu.expert_run(rows, x, want_f32=True)
+                yb, yfb = gpu.expert_run(tile, x, want_f32=True)
+                torch.cuda.synchronize()
+                assert torch.equal(yfa.view(torch.int32), yfb.view(torch.int32)), (T, dt)
+                assert torch.equal(ya.view(torch.int16), yb.view(torch.int16)), (T, dt)
     finally:
         rows.free()
         tile.free()
