@@ -948,7 +948,9 @@ int cx_upload_matrix(int device, const uint8_t* host_weight, uint64_t rows, uint
     hipError_t e = hipMemcpyAsync(pw, host_weight, wbytes, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipMemcpyAsync(ps, host_scale, sbytes, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = launch_canonicalize_fp8(static_cast<uint8_t*>(pw), wbytes, s);
-    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    // wait even after a failure: a copy queued before it may still write the blocks
+    const hipError_t es = hipStreamSynchronize(s);
+    if (e == hipSuccess) e = es;
     if (e != hipSuccess) {
         arena_free(device, pw, false);
         arena_free(device, ps, false);
@@ -992,7 +994,9 @@ int cx_upload_matrix_tiled(int device, const uint8_t* host_weight, uint64_t rows
     if (e == hipSuccess)
         e = launch_tile16_fp8(static_cast<const uint8_t*>(stage), static_cast<uint8_t*>(pw), (int)rows,
                               (int)cols, s);
-    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    // wait even after a failure: a copy queued before it may still write the stage block
+    const hipError_t es = hipStreamSynchronize(s);
+    if (e == hipSuccess) e = es;
     arena_free(device, stage, false);
     if (e != hipSuccess) {
         arena_free(device, pw, false);
