@@ -207,20 +207,30 @@ __device__ __forceinline__ Dc1Scales dc1_scales(const float* s_down, int down_rb
 // One wave's ring: NR routed stages (item weights pd, scales qd) then NS
 // shared stages (ps, qs); h of stage k read from the wave's LDS slice.  The
 // lane holds output rows 4g..4g+3 of the tile; each takes its own row
-// block's scale.
-template <int NR, int NS, int D, int NKB>
+// block's scale.  dma() issues the wave's h DMA after the first PRE weight
+// stages (PRE = 0: before any weight load).
+template <int NR, int NS, int D, int NKB, int PRE, class Dma>
 __device__ __forceinline__ void dc1_ring(const uint8_t* pd, const uint8_t* ps, Dc1Scales qd,
                                          Dc1Scales qs, const unsigned char* hw, int g,
-                                         f32x4* acc_r, f32x4* acc_s) {
+                                         f32x4* acc_r, f32x4* acc_s, Dma dma) {
     typedef Dc1Geom<NKB> G;
     constexpr int NK = NR + NS;
     constexpr int DP = D < NK ? D : NK;  // prologue stages
+    constexpr int P0 = PRE < DP ? PRE : DP;
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
     f32x4 ar = zero, as = zero;
     auto wptr = [&](int k) { return k < NR ? pd + k * kKB : ps + (k - NR) * kKB; };
     u32x4 wb[D][2];
 #pragma unroll
-    for (int s = 0; s < DP; ++s) {
+    for (int s = 0; s < P0; ++s) {
+        wb[s][0] = ld16(wptr(s));
+        wb[s][1] = ld16(wptr(s) + 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    dma();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = P0; s < DP; ++s) {
         wb[s][0] = ld16(wptr(s));
         wb[s][1] = ld16(wptr(s) + 16);
     }
@@ -237,10 +247,11 @@ __device__ __forceinline__ void dc1_ring(const uint8_t* pd, const uint8_t* ps, D
         hi_r[i] = 4 * g + i >= qd.split;
         hi_s[i] = 4 * g + i >= qs.split;
     }
-    // the DMA'd h is older than the ring's loads; nothing of the loop may
-    // move above this wait (the compiler cannot count LDS DMA exactly and
-    // would drain the ring with vmcnt(0))
-    vm_wait<2 * DP>();
+    // the DMA'd h (and the first P0 stages) are older than the remaining
+    // prologue loads; nothing of the loop may move above this wait (the
+    // compiler cannot count LDS DMA exactly and would drain the ring with
+    // vmcnt(0))
+    vm_wait<2 * (DP - P0)>();
     lds_dma_barrier();
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -277,7 +288,7 @@ __device__ __forceinline__ void dc1_ring(const uint8_t* pd, const uint8_t* ps, D
 // fetches the route table with the DMA, so the combine needs no memory
 // round trip.  With rows < 16, the MFMA's spare rows repeat the tile's last
 // weight row (the same addresses, so no extra bytes) and are not stored.
-template <int NKB, int D>
+template <int NKB, int D, int PRE = 0>
 __device__ __forceinline__ void down_comb1_tile(const ExpertLaunch& L, const int* token_pairs,
                                                 const float* topk_w, int top_k, unsigned char* lds,
                                                 int rtile, int rows) {
@@ -297,30 +308,34 @@ __device__ __forceinline__ void down_comb1_tile(const ExpertLaunch& L, const int
     const uint8_t* pd = nullptr;
     const uint8_t* ps = nullptr;
     Dc1Scales qd{nullptr, nullptr, kTileRows}, qs{nullptr, nullptr, kTileRows};
-    // 0) h into this wave's LDS slice (1 KB per wave instruction), before any weight load
+    // 0) h into this wave's LDS slice (1 KB per wave instruction), issued by
+    //    the ring after its first PRE weight stages
+    const uint16_t *hh = nullptr, *hl = nullptr, *hs = nullptr;
+    constexpr int LPP = G::kSharedBytes / 16;  // lanes per shared plane
     if (has_r) {
         const ItemRec ri = ld_uniform(L.plan.item_rec + wave);
-        const uint16_t* hh = L.h_hi + (size_t)ri.pb * I + lane * 8;
-        const uint16_t* hl = L.h_lo + (size_t)ri.pb * I + lane * 8;
-#pragma unroll
-        for (int j = 0; j < G::kRoutedBytes / 1024; ++j) {
-            __builtin_amdgcn_global_load_lds(hh + j * 512, hw + j * 1024, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(hl + j * 512, hw + G::kRoutedBytes + j * 1024, 16, 0, 0);
-        }
+        hh = L.h_hi + (size_t)ri.pb * I + lane * 8;
+        hl = L.h_lo + (size_t)ri.pb * I + lane * 8;
         pd = ri.w_down + (size_t)wr * I + g * 32;
         qd = dc1_scales(ri.s_down, ri.down_rb, r0, rows, I / kKB, 0);
     }
     if (has_s) {
         const ItemRec rs = ld_uniform(L.plan.item_rec + ts);
-        constexpr int LPP = G::kSharedBytes / 16;  // lanes per plane
         const size_t k0 = (size_t)wave * NKS * kKB;
-        if (lane < 2 * LPP) {
-            const uint16_t* src = (lane < LPP ? L.h_hi : L.h_lo) + (size_t)rs.pb * I + k0 + (lane % LPP) * 8;
-            __builtin_amdgcn_global_load_lds(src, hw + 2 * G::kRoutedBytes, 16, 0, 0);
-        }
+        hs = (lane < LPP ? L.h_hi : L.h_lo) + (size_t)rs.pb * I + k0 + (lane % LPP) * 8;
         ps = rs.w_down + (size_t)wr * I + k0 + g * 32;
         qs = dc1_scales(rs.s_down, rs.down_rb, r0, rows, I / kKB, wave * NKS);
     }
+    auto dma = [&] {
+        if (has_r) {
+#pragma unroll
+            for (int j = 0; j < G::kRoutedBytes / 1024; ++j) {
+                __builtin_amdgcn_global_load_lds(hh + j * 512, hw + j * 1024, 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(hl + j * 512, hw + G::kRoutedBytes + j * 1024, 16, 0, 0);
+            }
+        }
+        if (has_s && lane < 2 * LPP) __builtin_amdgcn_global_load_lds(hs, hw + 2 * G::kRoutedBytes, 16, 0, 0);
+    };
     // wave 0: the route table (lane k: pair and weight of route k), issued
     // with the DMA so that the ring's first wait covers it
     int tpl = -1;
@@ -331,9 +346,9 @@ __device__ __forceinline__ void down_comb1_tile(const ExpertLaunch& L, const int
     }
     __builtin_amdgcn_sched_barrier(0);
     f32x4 ar, as;
-    if (has_r && has_s) dc1_ring<NKB, NKS, D, NKB>(pd, ps, qd, qs, hw, g, &ar, &as);
-    else if (has_r) dc1_ring<NKB, 0, D, NKB>(pd, ps, qd, qs, hw, g, &ar, &as);
-    else if (has_s) dc1_ring<0, NKS, D, NKB>(pd, ps, qd, qs, hw, g, &ar, &as);
+    if (has_r && has_s) dc1_ring<NKB, NKS, D, NKB, PRE>(pd, ps, qd, qs, hw, g, &ar, &as, dma);
+    else if (has_r) dc1_ring<NKB, 0, D, NKB, PRE>(pd, ps, qd, qs, hw, g, &ar, &as, dma);
+    else if (has_s) dc1_ring<0, NKS, D, NKB, PRE>(pd, ps, qd, qs, hw, g, &ar, &as, dma);
     else {
         lds_dma_barrier();
         ar = as = f32x4{0.f, 0.f, 0.f, 0.f};

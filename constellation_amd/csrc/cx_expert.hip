@@ -463,12 +463,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 // ---------------------------------------------------------------------------
 // One-token decode: down projection of every item plus the weighted combine
 // (down_comb1_tile, cx_down.h), grid = hidden/rows workgroups of 8 waves.
-template <int NKB, int D>
+template <int NKB, int D, int PRE = 0>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_down_comb1(
     ExpertLaunch L, const int* __restrict__ token_pairs, const float* __restrict__ topk_w, int top_k,
     int rows) {
     extern __shared__ __attribute__((aligned(16))) unsigned char dc_lds[];
-    down_comb1_tile<NKB, D>(L, token_pairs, topk_w, top_k, dc_lds, blockIdx.x, rows);
+    down_comb1_tile<NKB, D, PRE>(L, token_pairs, topk_w, top_k, dc_lds, blockIdx.x, rows);
 }
 
 // ---------------------------------------------------------------------------

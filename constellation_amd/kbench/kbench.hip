@@ -347,6 +347,23 @@ int cmd_decode_down(int iters) {
     std::vector<DownPtrs> sets(16);
     for (auto& s : sets)
         for (int j = 0; j < 9; ++j) s.m[j] = pool.d[rng() % pool.d.size()].w_down;
+    {  // the orders of the h DMA give the same bits
+        const int rows = down_comb1_rows(kH, cus), grid = (kH + rows - 1) / rows;
+        std::vector<uint16_t> a(kH), b(kH);
+        int same = 0;
+        for (int i = 0; i < 4; ++i) {
+            ExpertLaunch L = dp.launch(i, table, lds);
+            L.skip_shared = 0;
+            L.max_items = 9;
+            KB_CHECK(launch_down_comb1(L, L.plan.token_pairs, dp.topk_w, 8, cus, 0));
+            KB_CHECK(hipMemcpy(a.data(), L.y, kH * 2, hipMemcpyDeviceToHost));
+            cx_launch(k_down_comb1<16, kDc1Depth, 2>, dim3(grid), dim3(64 * kDc1Waves), (uint32_t)down_comb1_lds(kI),
+                      (hipStream_t)0, L, (const int*)L.plan.token_pairs, (const float*)dp.topk_w, 8, rows);
+            KB_CHECK(hipMemcpy(b.data(), L.y, kH * 2, hipMemcpyDeviceToHost));
+            same += a == b;
+        }
+        std::printf("  k_down_comb1 with the h DMA after 2 stages: bit-identical in %d of 4 calls\n", same);
+    }
     for (int rep = 0; rep < 2; ++rep) {
         std::printf(" pass %d\n", rep + 1);
         report("bare stream, k_down_item shape (item x 64 rows)",
@@ -379,6 +396,19 @@ int cmd_decode_down(int iters) {
                    L.max_items = 9;
                    KB_CHECK(launch_down_comb1(L, L.plan.token_pairs, dp.topk_w, 8, cus, 0));
                }), down_bytes);
+        // the h DMA issued after the first PRE weight stages instead of before them
+        const int rows = down_comb1_rows(kH, cus), grid = (kH + rows - 1) / rows;
+        auto pre = [&](const char* what, auto kernel) {
+            report(what, time_launches(iters, [&](int i) {
+                       ExpertLaunch L = dp.launch(i, table, lds);
+                       L.skip_shared = 0;
+                       L.max_items = 9;
+                       cx_launch(kernel, dim3(grid), dim3(64 * kDc1Waves), (uint32_t)down_comb1_lds(kI),
+                                 (hipStream_t)0, L, (const int*)L.plan.token_pairs, (const float*)dp.topk_w, 8, rows);
+                   }), down_bytes);
+        };
+        pre("  k_down_comb1, h DMA after 2 weight stages", k_down_comb1<16, kDc1Depth, 2>);
+        pre("  k_down_comb1, h DMA after 4 weight stages", k_down_comb1<16, kDc1Depth, 4>);
         report("k_down_item (down, 9 items)", time_launches(iters, [&](int i) {
                    ExpertLaunch L = dp.launch(i, table, lds);
                    L.skip_shared = 0;
