@@ -204,28 +204,16 @@ class WorkerClient:
 HARNESS = __import__("pathlib").Path(__file__).resolve().parents[1] / "oracle" / "_ref" / "node_harness"
 
 
-def free_port_pair(offset: int = 100) -> tuple[int, int]:
-    """Two free local ports (control, worker base) whose worker base + offset is free too."""
-    for _ in range(50):
-        socks = [socket.socket() for _ in range(2)]
-        try:
-            for s in socks:
-                s.bind(("127.0.0.1", 0))
-            ctrl, wb = (s.getsockname()[1] for s in socks)
-        finally:
-            for s in socks:
-                s.close()
-        if wb + offset >= 65535 or ctrl in (wb + offset, wb + offset + 1):
-            continue
-        probe = socket.socket()
-        try:
-            probe.bind(("127.0.0.1", wb + offset))
-        except OSError:
-            continue
-        finally:
-            probe.close()
-        return ctrl, wb
-    raise RuntimeError("no free port pair")
+def free_port_pair() -> tuple[int, int]:
+    """Two free local ports: control, worker base (one GPU: one worker port)."""
+    socks = [socket.socket() for _ in range(2)]
+    try:
+        for s in socks:
+            s.bind(("127.0.0.1", 0))
+        return tuple(s.getsockname()[1] for s in socks)
+    finally:
+        for s in socks:
+            s.close()
 
 
 class Harness:

@@ -13,9 +13,11 @@ Covers, in order (one node process for the module):
     RunExpertRequest at fp16->fp16 B=1 (the server's wire,
     moe_layer_runtime.py:36-48) and bf16 B=4, the echo fields, and the
     status codes 1 / 2 / 4 of worker.cc:113-132;
-  * MoeLayerRequest on the integrated worker loop (HandleMoeLayerRequestAmdV2
-    -> RunMoeLayerRequest) bit-identical to cx_moe_layer_request_run in this
-    process on the same experts, and within the parity bound of the oracle;
+  * MoeLayerRequest on the reference's worker loop with the integration's
+    one branch (worker.cc streamed through oracle/integrate_worker.awk;
+    HandleMoeLayerRequestAmdV2 -> RunMoeLayerRequest) bit-identical to
+    cx_moe_layer_request_run in this process on the same experts, and within
+    the parity bound of the oracle; both message types on one connection;
   * uploads on the control thread while a worker connection infers;
   * replacement of a resident expert and a placement that drops residents
     (FreeExpertWeightsAmdV2);
@@ -58,10 +60,9 @@ class Node:
         self.experts[SHARED_ID] = oracle.gen_expert(500 + EPL, 0x40)
 
     def worker(self) -> WorkerClient:
-        return WorkerClient(self.h.wbase)          # the reference's RunGpuWorkerLoopV2
-
-    def layer_worker(self) -> WorkerClient:
-        return WorkerClient(self.h.wbase + 100)    # the loop with the MoeLayerRequest branch
+        # the reference's RunGpuWorkerLoopV2 with the integration's
+        # MoeLayerRequest branch: InferRequest and MoeLayerRequest on one port
+        return WorkerClient(self.h.wbase)
 
     def log(self) -> str:
         return self.log_path.read_text()
@@ -183,7 +184,7 @@ def test_moe_layer_request_equals_in_process(node, gpu, T, shared):
         "layer_id": LAYER, "batch_size": T, "hidden_dim": H, "top_k": K, "input_dtype": BF16,
         "output_dtype": BF16, "flags": P.FLAG_SHARED if shared else 0, "expert_ids": ids,
         "expert_weights": wts, "activation": _act(x, BF16)})
-    w = node.layer_worker()
+    w = node.worker()
     try:
         r = w.moe_layer(body)
     finally:
@@ -226,12 +227,16 @@ def test_moe_layer_request_status(node):
             "input_dtype": BF16, "output_dtype": BF16, "flags": flags,
             "expert_ids": np.asarray(ids, np.int32), "expert_weights": np.full(len(ids), 0.5, np.float32),
             "activation": act})
-    w = node.layer_worker()
+    w = node.worker()
     try:
         assert w.moe_layer(req([3, 300]))["status_code"] == 1       # local id beyond the layer
         assert w.moe_layer(req([3, 5]))["status_code"] == 2         # not resident here
         assert w.moe_layer(req([3], layer_id=7))["status_code"] == 2  # a layer with nothing here
         assert w.moe_layer(req([3], flags=P.FLAG_SHARED))["status_code"] == 0
+        # the same connection still serves the v1 message after the new one
+        r = w.infer(gid(3), 1, H, BF16, BF16, act)
+        assert r["status_code"] == 0 and len(r["output"]) == H * 2
+        assert w.moe_layer(req([3, 17]))["status_code"] == 0
     finally:
         w.close()
 
@@ -248,7 +253,7 @@ def test_remote_node_over_socket_equals_local_node(node, gpu):
     ids = np.stack([rng.choice(LOCAL, K, replace=False) for _ in range(T)]).astype(np.int32)
     wts = rng.uniform(0.1, 1.0, ids.shape).astype(np.float32)
     x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(torch.bfloat16).cuda()
-    w = node.layer_worker()
+    w = node.worker()
     local = {}
     try:
         remote = RemoteNode.over_socket(w.sock, {LAYER: LOCAL}, shared_layers=[LAYER])
