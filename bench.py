@@ -52,10 +52,11 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU baseline time budget")
     ap.add_argument("--no-extra-configs", action="store_true",
                     help="skip the single-expert, prefill and node-share measurements")
-    ap.add_argument("--extras", default="h,p,0,3,c,4",
+    ap.add_argument("--extras", default="h,p,g,0,3,c,4",
                     help="comma list of the extra measurements: h host boundary at B=1 "
                          "(layer request vs per-expert requests), p the B=1 layer through "
-                         "the fused and the staged pipeline (interleaved A/B), 0 single "
+                         "the fused and the staged pipeline (interleaved A/B), g the B=1 "
+                         "step eager vs replayed from a HIP graph (interleaved), 0 single "
                          "expert, 3 prefill chunk, c compute-bound prefill shape (not a "
                          "BASELINE config), 4 node share (default: all)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -156,6 +157,55 @@ def bench_b1_pipelines(ctx, layers, pool, steps, reps=3):
     return {name: {"us_per_token": statistics.median(r["wall"]),
                    "kernels_us": {k: statistics.median(v) for k, v in r["kernels"].items()}}
             for name, r in res.items()}
+
+
+def bench_b1_graph(ctx, layers, pool, reps=5):
+    """The B=1 layer step launched eagerly against the same 64 steps captured
+    once into a HIP graph (torch.cuda.CUDAGraph on a side stream) and
+    replayed 8 times, interleaved; medians over `reps` of the time per step.
+    The replayed outputs are first checked bit for bit against eager calls."""
+    import statistics
+    import torch
+    dev = pool.device
+
+    def mk():
+        return (torch.empty((1, H), dtype=torch.bfloat16, device=dev), None,
+                torch.empty((1, TOPK), dtype=torch.int32, device=dev),
+                torch.empty((1, TOPK), dtype=torch.float32, device=dev))
+    outs, ref = mk(), mk()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        run_steps(ctx, layers, pool, 1, 64, outs)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side, capture_error_mode="thread_local"):
+        run_steps(ctx, layers, pool, 1, 64, outs)
+    g.replay()
+    torch.cuda.synchronize()
+    run_steps(ctx, layers, pool, 1, 64, ref)
+    torch.cuda.synchronize()
+    equal = (torch.equal(outs[0].view(torch.int16), ref[0].view(torch.int16)) and
+             torch.equal(outs[2], ref[2]) and
+             torch.equal(outs[3].view(torch.int32), ref[3].view(torch.int32)))
+    res = {"eager": [], "graph": []}
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(reps):
+        ev0.record()
+        run_steps(ctx, layers, pool, 1, 512, outs)
+        ev1.record()
+        torch.cuda.synchronize()
+        res["eager"].append(ev0.elapsed_time(ev1) / 512 * 1e3)
+        ev0.record(side)
+        with torch.cuda.stream(side):
+            for _ in range(8):
+                g.replay()
+        ev1.record(side)
+        torch.cuda.synchronize()
+        res["graph"].append(ev0.elapsed_time(ev1) / 512 * 1e3)
+    del g
+    return {"eager_us_per_token": statistics.median(res["eager"]),
+            "graph_us_per_token": statistics.median(res["graph"]),
+            "replay_equals_eager": equal}
 
 
 def time_config(ctx, layers, pool, T, steps, warmup):
@@ -612,6 +662,8 @@ def main() -> int:
         extras["b1"]["host_boundary"] = bench_host_boundary(ctx, layers, pool, 100)
     if "p" in want:
         extras["b1"]["pipelines"] = bench_b1_pipelines(ctx, layers, pool, 400)
+    if "g" in want:
+        extras["b1"]["graph"] = bench_b1_graph(ctx, layers, pool)
     if "0" in want:
         extras["config0_single_expert"] = bench_single_expert(ctx, layers, max(100, args.steps // 2))
     if "3" in want:
