@@ -834,10 +834,11 @@ int cmd_grouped_down(int iters) {
 }
 
 int cmd_grouped(int iters) {
-    Pool pool(true);
+    Pool pool(true, CX_LAYOUT_TILE16);  // gate/up as the library uploads it
     std::vector<PrefillPlan> plans;
     for (int l = 0; l < 4; ++l) plans.emplace_back(pool, 5 + l);
-    std::printf("grouped: config-3-like plan, %d items, experts spread over 24 x 2 GiB\n", plans[0].n_items);
+    std::printf("grouped: config-3-like plan, %d items, experts spread over 24 x 2 GiB, tiled gate/up\n",
+                plans[0].n_items);
     const double gu = 257.0 * 2 * kMat + 512.0 * kH * 2;
     const double dn = 257.0 * kMat + 4608.0 * kH * 4;
     for (int rep = 0; rep < 2; ++rep) {
