@@ -341,6 +341,45 @@ def test_moe_layer_fused_router(gpu, oracle):
         _free(layer, experts, sh)
 
 
+@pytest.mark.parametrize("T,norm,scale,K", [(1, False, 1.0, 8), (1, True, 1.7, 1), (1, False, 2.5, 4),
+                                             (3, False, 2.5, 6), (40, False, 0.5, 8)])
+def test_moe_layer_router_options(gpu, oracle, T, norm, scale, K):
+    """Router options beyond DeepSeek-V3's defaults through cx_moe_layer:
+    weights left unnormalised, other routed scaling factors and a single
+    pick (no normalisation at k = 1, server/moe_layer_runtime.py:376-379).  T = 1
+    takes the one-token pipeline (selection inside the routed gate/up), T = 3
+    the staged decode pipeline, T = 40 the grouped prefill path; routes and
+    weights against the oracle's, output within the parity bound."""
+    print(f"[moe] router options T={T} norm={norm} scale={scale} K={K}", flush=True)
+    E, H, I = 256, 1024, 512
+    layer, experts, sh, cpu, cpu_sh = _make_layer(gpu, oracle, E, H, I, seed=130 + T)
+    try:
+        x, w, bias = _router_inputs(gpu, 131 + T + K, T, E, H)
+        y, yf, ids, wts = gpu.moe_layer(layer, x, w, bias, n_group=8, topk_group=4, top_k=K,
+                                        norm_topk_prob=norm, routed_scaling_factor=scale,
+                                        want_f32=True)
+        gpu.sync()
+        checked = 0
+        for t, (oi, ow, margins, _) in enumerate(_oracle_route(oracle, x, w, bias, top_k=K,
+                                                               norm=norm, scale=scale)):
+            if min(margins) <= 1e-12:
+                continue
+            assert ids[t].cpu().tolist() == oi.tolist(), t
+            assert np.allclose(wts[t].cpu().numpy(), ow, rtol=1e-6, atol=0), t
+            checked += 1
+        assert checked >= T - 1
+        if not norm and K > 1:
+            # unnormalised: each weight is scale * sigmoid(logit), never a share of 1
+            assert not np.allclose(wts.sum(dim=1).cpu().numpy(), scale, rtol=1e-3)
+        ref = _oracle_moe(oracle, cpu, cpu_sh, x.float().cpu().numpy(), ids.cpu().numpy(),
+                          wts.cpu().numpy())
+        yf = yf.cpu().numpy()
+        assert rel_l2(yf, ref) < 1e-5, rel_l2(yf, ref)
+        assert np.array_equal(_bits(y), oracle.encode_act(yf, BF16, "rne"))
+    finally:
+        _free(layer, experts, sh)
+
+
 def test_moe_layer_decode_back_to_back(gpu, oracle):
     """The decode pipeline (T <= 16) reuses its plan, h, k-part and y_part
     buffers on every call.  Twelve calls back to back with new tokens (and
