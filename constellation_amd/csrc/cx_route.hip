@@ -1608,14 +1608,14 @@ struct SelArgs {
 
 // The routes (weights as select_reg forms them: s of the picks normalised
 // by their sum in pick order, + 1e-20, then scaled) and the one-token plan
-// the down + combine launch reads (down_comb1_tile): routed item i = the
-// pick with the i-th smallest expert id (the planner's slot order) owns
-// pair s0 + i, the shared expert pair 0; token_pairs[k] = pair of route k
-// (column top_k: the shared pair).  Lane r < top_k holds pick r and its id
-// rank.
+// the down + combine launch reads (down_comb1_tile): routed item i = pick i
+// (descending choice score) owns pair s0 + i, the shared expert pair 0;
+// token_pairs[k] = pair of route k (column top_k: the shared pair).  Lane
+// r < top_k holds pick r.  The combine sums in route order, so the item
+// order changes no output bit.
 __device__ __forceinline__ void dec_sel_plan(const ExpertLaunch& L, const SelArgs& S, int isel,
-                                             int rank, int s0) {
-    const int lane = threadIdx.x & 63, K = S.top_k;
+                                             int s0) {
+    const int lane = threadIdx.x & 63, K = S.top_k, rank = lane;
     const double sv = lane < K ? S.sc[isel] : 0.0;
     double wsum = 0.0;
     for (int r = 0; r < K; ++r) wsum += readlane_d(sv, r);
@@ -1645,12 +1645,12 @@ __device__ __forceinline__ void dec_sel_plan(const ExpertLaunch& L, const SelArg
 
 // Stage 2: grid (inter / 16 row tiles, top_k picks [+ 1]).  Wave 0 of every
 // workgroup selects (select256 on stage 1's choice scores: the same inputs
-// and code everywhere, so every workgroup finds the same picks), numbers the
-// picks by ascending expert id and hands pick blockIdx.y's expert to the
-// other waves through LDS; the workgroup then streams row tile blockIdx.x of
-// that expert's gate and up (gate_up_tile_unit, x staged in LDS).  With a
-// shared expert, the last grid row finalises its h from stage 1's k-part
-// sums.
+// and code everywhere, so every workgroup finds the same picks) as far as
+// pick blockIdx.y, whose expert it hands to the other waves through LDS
+// (rows of early picks start streaming earlier); the workgroup then streams
+// row tile blockIdx.x of that expert's gate and up (gate_up_tile_unit, x
+// staged in LDS).  With a shared expert, the last grid row finalises its h
+// from stage 1's k-part sums.
 template <int NKB>
 __global__ __launch_bounds__(256) void k_gate_up_sel(ExpertLaunch L, SelArgs S) {
     extern __shared__ __attribute__((aligned(16))) unsigned char gu_lds[];
@@ -1673,17 +1673,14 @@ __global__ __launch_bounds__(256) void k_gate_up_sel(ExpertLaunch L, SelArgs S) 
             c[3] = __longlong_as_double((static_cast<long long>(v1[3]) << 32) | v1[2]);
         }
         groups256(c, S.topk_group);
-        const Picks8 p = picks256(c, K);
-        int isel = -1;  // lane r < K: pick r
+        // grid row y takes pick y, so it needs picks 0..y only; the last
+        // row's workgroup 0 has them all and writes the plan
+        const Picks8 p = picks256(c, min(item + 1, K));
+        int isel = -1;  // lane r <= item: pick r
 #pragma unroll
         for (int r = 0; r < kSel256MaxPicks; ++r) isel = lane == r ? p.id[r] : isel;
-        int rank = 0;  // of this lane's pick among the picks, by expert id
-#pragma unroll
-        for (int r = 0; r < kSel256MaxPicks; ++r) rank += (r < K && p.id[r] < isel) ? 1 : 0;
-        const unsigned long long hit = __ballot(lane < K && rank == item);
-        if (lane == 0)
-            s_expert = item < K ? __builtin_amdgcn_readlane(isel, static_cast<int>(__builtin_ctzll(hit))) : -1;
-        if (blockIdx.x == 0 && item == 0) dec_sel_plan(L, S, isel, rank, s0);
+        if (lane == 0) s_expert = item < K ? __builtin_amdgcn_readlane(isel, item) : -1;
+        if (blockIdx.x == 0 && item == K - 1) dec_sel_plan(L, S, isel, s0);
     }
     __syncthreads();
     const int e = __builtin_amdgcn_readfirstlane(s_expert);
