@@ -663,7 +663,11 @@ def main() -> int:
     if "p" in want:
         extras["b1"]["pipelines"] = bench_b1_pipelines(ctx, layers, pool, 400)
     if "g" in want:
-        extras["b1"]["graph"] = bench_b1_graph(ctx, layers, pool)
+        try:
+            extras["b1"]["graph"] = bench_b1_graph(ctx, layers, pool)
+        except RuntimeError as e:  # a capture the runtime refuses: report it, keep the line
+            torch.cuda.synchronize()
+            extras["b1"]["graph"] = {"error": str(e)[:200]}
     if "0" in want:
         extras["config0_single_expert"] = bench_single_expert(ctx, layers, max(100, args.steps // 2))
     if "3" in want:
